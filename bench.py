@@ -1,0 +1,297 @@
+"""Benchmark of the gtx16_fp16 GEMM hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--report FILE]
+
+Prints ONE JSON line for the BASELINE metric "TFLOPS (% MFMA peak) at 4096^3; GB/s (% HBM peak)
+for M=1 4096x4096 mm_t":
+
+* ``value`` -- TFLOPS of ``gtx16_fp16.mm_t`` on the 4096^3 configuration with fp32 activations
+  (1% of rows pushed to |max| in [2e3, 2e5], so the power-of-two row rescale is exercised) and
+  fp16 weights, fp32 out: one step = one mm_t call (rowscale cast + MFMA GEMM), inputs resident in
+  HBM, ``steps`` calls timed between two ``torch.cuda.synchronize()``.
+* ``roofline`` -- the GEMM kernel alone (the dominant kernel): 2*M*N*K flop per launch divided by
+  its average launch duration from HIP events around ``steps`` back-to-back launches on the
+  stream the kernel runs on, against the fp16 dense MFMA peak.
+* ``skinny_m1`` -- the second half of the metric: GB/s of the M=1 K=N=4096 skinny path, kernel
+  time from HIP events around a captured HIP graph of launches that rotate over 16 distinct 32 MiB
+  weight copies (512 MiB, twice the 256 MB Infinity Cache, so bytes come from HBM), against the
+  8 TB/s HBM peak; plus the per-call mm_t time.
+* ``cpu_baseline`` -- the reference's CPU path (torch fp32 matmul, the fallback of ops.py:119)
+  on a 4096^3 sample on the host cores of the same run.
+
+Inputs are synthetic and seeded on the CPU (x = seed 0, w = 1, bias = 2, outlier rows = 3).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (str(REPO), str(REPO / "gtx16-fp16_amd"), str(REPO / "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 flop/clk/CU (dense fp16)
+HBM_PEAK_GBS = 8000.0
+METRIC = "TFLOPS (% MFMA peak) at 4096^3; GB/s (% HBM peak) for M=1 4096x4096 mm_t"
+
+
+def parse(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--report", type=str, default=None, help="also write per-kernel details to this JSON file")
+    return ap.parse_args(argv)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def event_time_ms(fn, reps: int, torch) -> float:
+    """Average ms per call of ``fn`` from HIP events on torch's current stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def bench_c4(torch, g, lib, steps: int, warmup: int, dev) -> dict:
+    from _inputs import outlier_rows, randn
+
+    M = K = N = 4096
+    x = outlier_rows(randn((M, K), seed=0), 0.01, 2e3, 2e5, seed=3).to(dev)
+    w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(dev)
+    flop = 2.0 * M * N * K
+
+    for _ in range(warmup):
+        g.mm_t(x, w, None, torch.float32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.mm_t(x, w, None, torch.float32)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+
+    # Kernel-level timing on the stream the kernels are launched on (torch's current stream).
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    x16 = torch.empty(M, K, dtype=torch.float16, device=dev)
+    rs = torch.empty(M, dtype=torch.float32, device=dev)
+    out = torch.empty(M, N, dtype=torch.float32, device=dev)
+
+    def rowscale():
+        lib.g16_rowscale_f32(x.data_ptr(), x16.data_ptr(), rs.data_ptr(), M, K, 1024.0, stream)
+
+    def gemm():
+        lib.g16_hgemm_f32out(x16.data_ptr(), w.data_ptr(), out.data_ptr(), None, rs.data_ptr(), M, N, K, stream)
+
+    rowscale()
+    for _ in range(warmup):
+        gemm()
+    torch.cuda.synchronize()
+    gemm_ms = min(event_time_ms(gemm, steps, torch) for _ in range(3))
+    rowscale_ms = min(event_time_ms(rowscale, steps, torch) for _ in range(3))
+    tflops = flop / (wall_ms * 1e-3) / 1e12
+    gemm_tflops = flop / (gemm_ms * 1e-3) / 1e12
+    # rowscale: reads 64 MiB fp32, writes 32 MiB fp16 + 16 KiB of scales
+    rs_bytes = M * K * 4 + M * K * 2 + M * 4
+    return {
+        "wall_ms_per_step": wall_ms,
+        "tflops": tflops,
+        "gemm_kernel_ms": gemm_ms,
+        "gemm_kernel_tflops": gemm_tflops,
+        "rowscale_kernel_ms": rowscale_ms,
+        "rowscale_kernel_gbs": rs_bytes / (rowscale_ms * 1e-3) / 1e9,
+        "flop_per_step": flop,
+        "outlier_rows": int(round(0.01 * M)),
+    }
+
+
+def bench_skinny(torch, lib, g, steps: int, warmup: int, dev, copies: int = 16) -> dict:
+    from _inputs import randn
+
+    M, K, N = 1, 4096, 4096
+    x = randn((M, K), seed=0).to(dev)
+    b = randn((N,), seed=2, scale=0.02).to(dev)
+    w0 = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(dev)
+    # distinct allocations of the weight, so consecutive launches never find it in a cache
+    ws = [w0.clone() for _ in range(copies)]
+    nbytes = M * K * 4 + K * N * 2 + N * 4 + M * N * 4
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    ksplit = lib.g16_skinny_plan(M, N, K, cus)
+    work = torch.empty(max(lib.g16_skinny_workspace_bytes(M, N, K, ksplit), 256), dtype=torch.uint8, device=dev)
+    cnt = torch.zeros(max(lib.g16_skinny_counter_bytes(M, N, K, ksplit), 256), dtype=torch.uint8, device=dev)
+    out = torch.empty(M, N, dtype=torch.float32, device=dev)
+
+    # per-call wall time of the Python API, rotating the weight copies
+    for i in range(warmup):
+        g.mm_t(x, ws[i % copies], b, torch.float32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    calls = max(steps, copies)
+    for i in range(calls):
+        g.mm_t(x, ws[i % copies], b, torch.float32)
+    torch.cuda.synchronize()
+    call_us = (time.perf_counter() - t0) * 1e6 / calls
+
+    # kernel time: a HIP graph of `copies` launches, replayed between events
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        st = side.cuda_stream
+        for wi in ws:  # warm the exact launches once before capture
+            assert lib.g16_skinny_f32in(x.data_ptr(), wi.data_ptr(), out.data_ptr(), b.data_ptr(), M, N, K, ksplit,
+                                        work.data_ptr(), work.numel(), cnt.data_ptr(), cnt.numel(), st) == 0
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            cap = torch.cuda.current_stream(dev).cuda_stream
+            for wi in ws:
+                lib.g16_skinny_f32in(x.data_ptr(), wi.data_ptr(), out.data_ptr(), b.data_ptr(), M, N, K, ksplit,
+                                     work.data_ptr(), work.numel(), cnt.data_ptr(), cnt.numel(), cap)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    reps = max(4, steps // 4)
+    per_launch = []
+    for _ in range(3):
+        ms = event_time_ms(graph.replay, reps, torch)
+        per_launch.append(ms / copies)
+    kern_ms = min(per_launch)
+    return {
+        "M": M, "K": K, "N": N,
+        "ksplit": ksplit,
+        "bytes_per_launch": nbytes,
+        "kernel_us": kern_ms * 1e3,
+        "kernel_gbs": nbytes / (kern_ms * 1e-3) / 1e9,
+        "call_us": call_us,
+        "call_gbs": nbytes / (call_us * 1e-6) / 1e9,
+        "weight_copies": copies,
+        "weight_bytes_rotated": copies * K * N * 2,
+    }
+
+
+def cpu_baseline(torch) -> dict:
+    """The reference's CPU path: torch fp32 matmul (ops.py:119 fallback) at 4096^3 on the host."""
+    from _inputs import outlier_rows, randn
+
+    M = K = N = 4096
+    x = outlier_rows(randn((M, K), seed=0), 0.01, 2e3, 2e5, seed=3)
+    w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).float()
+    torch.matmul(x, w)  # warm-up
+    times = []
+    t_end = time.perf_counter() + 10.0
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 30):
+        t0 = time.perf_counter()
+        torch.matmul(x, w)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": 2.0 * M * N * K / med / 1e12,
+        "unit": "TFLOPS",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": (f"torch fp32 x@w at M=K=N=4096 on the host (the reference's CPU path: ops.py:119 "
+                   f"fallback), 1 warm-up + median of {len(times)} reps; cpu '{cpu_model()}', "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def main(argv=None) -> int:
+    args = parse(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the GEMM path "
+              "has no multi-GPU component to time. Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    import gtx16_fp16 as g
+    from gtx16_fp16 import _clib
+
+    lib = _clib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev)
+    sk = bench_skinny(torch, lib, g, args.steps, args.warmup, dev)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(torch)
+
+    gemm_tflops = c4["gemm_kernel_tflops"]
+    line = {
+        "metric": METRIC,
+        "value": round(c4["tflops"], 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c4["wall_ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (fp32 accumulate)",
+        "data": "synthetic (seeded CPU randn: x fp32 with 1% outlier rows, w fp16 ~N(0,0.02^2))",
+        "config": {"workload": "mm_t C4: M=K=N=4096, fp32 activations + pow2 rowscale, fp16 weights, fp32 out",
+                   "M": 4096, "K": 4096, "N": 4096, "outlier_rows": c4["outlier_rows"]},
+        "pct_of_peak": round(100.0 * c4["tflops"] / MFMA_F16_PEAK_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "hgemm_kernel<256x256> (g16_hgemm_f32out)",
+            "achieved": round(gemm_tflops, 2),
+            "peak": MFMA_F16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "kernel_ms": round(c4["gemm_kernel_ms"], 5),
+        },
+        "rowscale_kernel": {"ms": round(c4["rowscale_kernel_ms"], 5), "GB/s": round(c4["rowscale_kernel_gbs"], 1),
+                            "frac_hbm": round(c4["rowscale_kernel_gbs"] / HBM_PEAK_GBS, 4)},
+        "skinny_m1": {
+            "workload": "mm_t M=1 K=N=4096, fp32 x, fp16 w_t, fp32 bias, fp32 out (16 rotated weight copies)",
+            "value": round(sk["kernel_gbs"], 1),
+            "unit": "GB/s",
+            "pct_of_peak": round(100.0 * sk["kernel_gbs"] / HBM_PEAK_GBS, 2),
+            "roofline": {
+                "bound": "hbm",
+                "kernel": "skinny_kernel<float,1> (g16_skinny_f32in)",
+                "achieved": round(sk["kernel_gbs"], 1),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(sk["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": None,
+                "kernel_us": round(sk["kernel_us"], 3),
+            },
+            "bytes_per_launch": sk["bytes_per_launch"],
+            "ksplit": sk["ksplit"],
+            "mm_t_call_us": round(sk["call_us"], 2),
+        },
+        "cpu_baseline": cpu,
+    }
+    if args.report:
+        Path(args.report).write_text(json.dumps({"c4": c4, "skinny_m1": sk, "cpu": cpu}, indent=2))
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,106 @@
+// Shared helpers for the gfx950 kernels of libg16.so: vector types, launch wrapper, argument
+// checks, and the cross-workgroup "last arrival" handshake used by the deterministic split
+// reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "g16.h"
+
+namespace g16 {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+template <typename T>
+struct identity {
+  using type = T;
+};
+
+// Launch `kern` with hipLaunchKernel so the launch status comes back as a value (a positive
+// hipError_t), not through the sticky per-thread error state.
+template <typename... KArgs>
+static inline int launch(void (*kern)(KArgs...), dim3 grid, dim3 block, hipStream_t stream,
+                         typename identity<KArgs>::type... args) {
+  void* argv[] = {static_cast<void*>(&args)...};
+  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(kern), grid, block, argv, 0, stream);
+  return static_cast<int>(err);
+}
+
+static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Per-tile arrival counters at the head of a workspace, one per 256 bytes: counters that share a
+// cache line serialize their atomics in one memory-side atomic unit, and every workgroup of a
+// split kernel arrives at about the same time.
+constexpr int kCounterStride = 64;  // uint32 elements between consecutive counters
+static inline size_t counter_bytes(size_t ntiles) { return ntiles * kCounterStride * sizeof(uint32_t); }
+
+__host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// ---- data exchanged between the workgroups of one kernel (split reductions) ----
+//
+// A workgroup publishes its partial sums, then bumps a per-tile arrival counter; the workgroup
+// that arrives last adds everything up. The partials are written and read with device-coherent
+// accesses (agent-scope atomic loads/stores for 4 bytes, buffer accesses with the sc1 cache
+// policy for 16 bytes -- the same instructions), which bypass the XCD-private L2 state. Ordering
+// then needs no agent-scope release/acquire fence (those write back and invalidate the whole L2
+// of every XCD and cost several microseconds per workgroup): each thread waits for its own
+// coherent stores to complete before the workgroup barrier, the counter increment follows the
+// barrier, and the last arriver issues its coherent loads only after it has seen the final count.
+
+__device__ inline void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kCpolSc1 = 16;                   // cache policy bits: sc1 (device coherent)
+constexpr int kRawBufferDword3 = 0x00020000;   // raw (untyped) buffer descriptor word 3
+
+// A buffer resource over [base, base + bytes) for 16-byte coherent accesses (bytes < 2^31).
+__device__ inline __amdgpu_buffer_rsrc_t coherent_rsrc(void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(bytes), kRawBufferDword3);
+}
+__device__ inline void store_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4v v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, static_cast<int>(byte_off), 0, kCpolSc1);
+}
+__device__ inline float4v load_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_off), 0, kCpolSc1));
+}
+
+// Every thread of the workgroup calls this after its coherent stores. Returns true in every
+// thread of the workgroup that arrives last for `counter` (the expected-th arrival); that
+// workgroup must call reset_counter() so the counter is zero again for the next launch.
+__device__ inline bool arrive_last_coherent(uint32_t* counter, uint32_t expected) {
+  __shared__ uint32_t s_last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed at the coherence point
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev + 1u == expected) ? 1u : 0u;
+  }
+  __syncthreads();
+  return s_last != 0u;
+}
+
+__device__ inline void reset_counter(uint32_t* counter) {
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline float h2f(_Float16 h) { return static_cast<float>(h); }
+__device__ inline float to_f(float x) { return x; }
+__device__ inline float to_f(_Float16 x) { return static_cast<float>(x); }
+
+}  // namespace g16

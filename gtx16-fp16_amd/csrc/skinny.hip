@@ -1,0 +1,257 @@
+// Skinny GEMM for 1 <= M <= 8 (token-by-token decode): C[M,N] = A[M,K] @ B[K,N] + bias.
+//
+// Semantics (reference: src/gtx16_fp16/kernels.py:153-219, ops.py:45-51,78-84): fp32 math on the
+// unquantised activations (fp32 or fp16 used as is), fp16 weights widened to fp32, bias added once,
+// fp32 output.
+//
+// The path is HBM-bound for small M (arithmetic intensity <= 8 flop/byte): B is streamed exactly
+// once and the design follows from B's layout ([K,N], N contiguous):
+//   * A workgroup (8 wavefronts) owns a 512-column strip of B and a slice of K rows. Each
+//     wavefront takes a contiguous run of rows; one load instruction reads one 1 KB row segment
+//     (64 lanes x 16 bytes = 512 fp16 columns), so every load is fully coalesced and the
+//     activation A[m,k] it multiplies is the same for the whole wavefront: A comes in through
+//     scalar loads, and the vector memory path carries nothing but B.
+//   * Each lane issues kU row loads before it uses any, so a workgroup has 128 KB of B in
+//     flight: enough to cover HBM latency with about one workgroup per CU.
+//   * Reduction is fixed-order: the wavefronts' partial rows are added in wavefront order through
+//     LDS; when K is split over several workgroups, each slice publishes its 512 x M partial with
+//     device-coherent stores and the last slice to arrive (per strip) adds the slices in slice
+//     order. No floating-point atomics: results are bitwise reproducible and C needs no zero-fill
+//     (the reference zero-fills C and accumulates with atomicAdd, kernels.py:205-206).
+#include "g16_common.hpp"
+
+namespace g16 {
+namespace {
+
+constexpr int kStripCols = 512;  // 64 lanes x 8 fp16 columns
+constexpr int kWaves = 8;        // wavefronts per workgroup
+constexpr int kThreads = kWaves * kWave;
+constexpr int kU = 16;           // rows per wavefront per unrolled step
+
+__device__ inline float x_at(const float* __restrict__ A, size_t i) { return A[i]; }
+// fp16 activations are read as the aligned dword holding them, so the (wavefront-uniform) load
+// stays a scalar load.
+__device__ inline float x_at(const _Float16* __restrict__ A, size_t i) {
+  const uint32_t d = reinterpret_cast<const uint32_t*>(A)[i >> 1];
+  const half2v h = __builtin_bit_cast(half2v, d);
+  return static_cast<float>((i & 1) ? h.y : h.x);
+}
+
+template <int MM>
+__device__ inline void fma_row(float (&acc)[MM][8], const float (&a)[MM], u32x4 w) {
+  float wf[8];
+  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const half2v h = __builtin_bit_cast(half2v, d[q]);
+    wf[2 * q] = static_cast<float>(h.x);
+    wf[2 * q + 1] = static_cast<float>(h.y);
+  }
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[m][j] = fmaf(a[m], wf[j], acc[m][j]);
+}
+
+template <typename TX, int MM>
+__global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__ A, const _Float16* __restrict__ B,
+                                                          float* __restrict__ C, const float* __restrict__ bias,
+                                                          float* __restrict__ part, uint32_t* __restrict__ counters,
+                                                          int N, int K, int rows_per_wave, int ksplit, int nstrips) {
+  __shared__ float red[kWaves][kStripCols];
+  const int strip = blockIdx.x % nstrips;
+  const int kpart = blockIdx.x / nstrips;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = strip * kStripCols + lane * 8;
+  const int k0 = (kpart * kWaves + wave) * rows_per_wave;
+  const int k1 = min(K, k0 + rows_per_wave);
+
+  float acc[MM][8];
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[m][j] = 0.f;
+
+  if (col < N) {
+    const _Float16* bp = B + col;
+    int k = k0;
+    for (; k + kU <= k1; k += kU) {
+      u32x4 w[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) w[u] = *reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(k + u) * N);
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        float a[MM];
+#pragma unroll
+        for (int m = 0; m < MM; ++m) a[m] = x_at(A, static_cast<size_t>(m) * K + k + u);
+        fma_row<MM>(acc, a, w[u]);
+      }
+    }
+    for (; k < k1; ++k) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(k) * N);
+      float a[MM];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) a[m] = x_at(A, static_cast<size_t>(m) * K + k);
+      fma_row<MM>(acc, a, w);
+    }
+  }
+
+  // Wavefronts -> thread t owns column strip*512 + t; sum the wavefronts in order.
+  const int t = threadIdx.x;
+  const int c = strip * kStripCols + t;
+  float mine[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    *reinterpret_cast<float4v*>(&red[wave][lane * 8]) = float4v{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+    *reinterpret_cast<float4v*>(&red[wave][lane * 8 + 4]) = float4v{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
+    __syncthreads();
+    float s = red[0][t];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) s += red[w][t];
+    mine[m] = s;
+    __syncthreads();
+  }
+
+  if (ksplit == 1) {
+    if (c < N) {
+      const float b = bias ? bias[c] : 0.f;
+#pragma unroll
+      for (int m = 0; m < MM; ++m) C[static_cast<size_t>(m) * N + c] = mine[m] + b;
+    }
+    return;
+  }
+
+  if (c < N) {
+#pragma unroll
+    for (int m = 0; m < MM; ++m) store_coherent(part + (static_cast<size_t>(kpart) * MM + m) * N + c, mine[m]);
+  }
+  if (!arrive_last_coherent(counters + strip * kCounterStride, static_cast<uint32_t>(ksplit))) return;
+  if (c < N) {
+    // Slices are added in slice order; loads are issued kZBatch slices at a time so their
+    // latencies overlap. Every slice, this one's included, is read back from the workspace.
+    constexpr int kZBatch = 8;
+    float s[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) s[m] = 0.f;
+    for (int z0 = 0; z0 < ksplit; z0 += kZBatch) {
+      float v[kZBatch][MM];
+#pragma unroll
+      for (int b = 0; b < kZBatch; ++b)
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+          v[b][m] = z0 + b < ksplit ? load_coherent(part + (static_cast<size_t>(z0 + b) * MM + m) * N + c) : 0.f;
+#pragma unroll
+      for (int b = 0; b < kZBatch; ++b)
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+          if (z0 + b < ksplit) s[m] += v[b][m];
+    }
+    const float bb = bias ? bias[c] : 0.f;
+#pragma unroll
+    for (int m = 0; m < MM; ++m) C[static_cast<size_t>(m) * N + c] = s[m] + bb;
+  }
+  reset_counter(counters + strip * kCounterStride);
+}
+
+struct Split {
+  int ksplit;         // slices actually launched
+  int rows_per_wave;  // K rows per wavefront (a slice is kWaves times that)
+};
+
+Split split_for(int K, int ksplit) {
+  if (K <= 0) return {1, 0};
+  if (ksplit < 1) ksplit = 1;
+  const int rpw = ceil_div(ceil_div(K, ksplit), kWaves);
+  return {ceil_div(K, rpw * kWaves), rpw};
+}
+
+template <typename TX>
+using SkinnyFn = void (*)(const TX*, const _Float16*, float*, const float*, float*, uint32_t*, int, int, int, int, int);
+
+template <typename TX>
+SkinnyFn<TX> skinny_fn(int M) {
+  switch (M) {
+    case 1: return skinny_kernel<TX, 1>;
+    case 2: return skinny_kernel<TX, 2>;
+    case 3: return skinny_kernel<TX, 3>;
+    case 4: return skinny_kernel<TX, 4>;
+    case 5: return skinny_kernel<TX, 5>;
+    case 6: return skinny_kernel<TX, 6>;
+    case 7: return skinny_kernel<TX, 7>;
+    default: return skinny_kernel<TX, 8>;
+  }
+}
+
+size_t workspace_bytes(int M, int N, int ksplit) {
+  if (ksplit <= 1 || M <= 0 || N <= 0) return 0;
+  return static_cast<size_t>(ksplit) * M * N * sizeof(float);
+}
+
+size_t counters_needed(int M, int N, int ksplit) {
+  if (ksplit <= 1 || M <= 0 || N <= 0) return 0;
+  return counter_bytes(static_cast<size_t>(ceil_div(N, kStripCols)));
+}
+
+template <typename TX>
+int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, int M, int N, int K, int ksplit,
+                  void* ws, size_t ws_bytes, uint32_t* counters_in, size_t counter_bytes_in, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || M > G16_SKINNY_MAX_M || K % 8 != 0 || N % 8 != 0) return G16_E_SHAPE;
+  if (M == 0 || N == 0) return G16_OK;
+  if (ksplit < 1 || ksplit > 4096) return G16_E_SPLIT;
+  if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return G16_E_NULL;
+  if (!aligned16(A) || !aligned16(B)) return G16_E_ALIGN;
+  const Split sp = split_for(K, ksplit);
+  const int nstrips = ceil_div(N, kStripCols);
+  float* part = nullptr;
+  uint32_t* counters = nullptr;
+  if (sp.ksplit > 1) {
+    if (ws == nullptr || ws_bytes < workspace_bytes(M, N, sp.ksplit)) return G16_E_WORKSPACE;
+    if (counters_in == nullptr || counter_bytes_in < counters_needed(M, N, sp.ksplit)) return G16_E_WORKSPACE;
+    if (!aligned16(ws) || !aligned16(counters_in)) return G16_E_ALIGN;
+    counters = counters_in;
+    part = static_cast<float*>(ws);
+  }
+  const dim3 grid(static_cast<unsigned>(nstrips) * static_cast<unsigned>(sp.ksplit)), block(kThreads);
+  return launch(skinny_fn<TX>(M), grid, block, static_cast<hipStream_t>(stream), A,
+                reinterpret_cast<const _Float16*>(B), C, bias, part, counters, N, K, sp.rows_per_wave, sp.ksplit,
+                nstrips);
+}
+
+}  // namespace
+}  // namespace g16
+
+extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
+  // About one 8-wavefront workgroup per CU, each wavefront streaming >= kU rows when K allows.
+  (void)M;
+  if (N <= 0 || K <= 0 || num_cus <= 0) return 1;
+  const int nstrips = g16::ceil_div(N, g16::kStripCols);
+  int ks = g16::ceil_div(num_cus, nstrips);
+  const int cap = K / (g16::kWaves * g16::kU) > 1 ? K / (g16::kWaves * g16::kU) : 1;
+  ks = ks < 1 ? 1 : (ks > cap ? cap : ks);
+  return g16::split_for(K, ks).ksplit;
+}
+
+extern "C" size_t g16_skinny_workspace_bytes(int M, int N, int K, int ksplit) {
+  if (K <= 0) return 0;
+  return g16::workspace_bytes(M, N, g16::split_for(K, ksplit).ksplit);
+}
+
+extern "C" size_t g16_skinny_counter_bytes(int M, int N, int K, int ksplit) {
+  if (K <= 0) return 0;
+  return g16::counters_needed(M, N, g16::split_for(K, ksplit).ksplit);
+}
+
+extern "C" int g16_skinny_f32in(const float* A, const uint16_t* B, float* C, const float* bias, int M, int N, int K,
+                                int ksplit, void* workspace, size_t workspace_bytes, uint32_t* counters,
+                                size_t counter_bytes, void* stream) {
+  return g16::skinny_launch<float>(A, B, C, bias, M, N, K, ksplit, workspace, workspace_bytes, counters, counter_bytes,
+                                   stream);
+}
+
+extern "C" int g16_skinny_f16in(const uint16_t* A, const uint16_t* B, float* C, const float* bias, int M, int N,
+                                int K, int ksplit, void* workspace, size_t workspace_bytes, uint32_t* counters,
+                                size_t counter_bytes, void* stream) {
+  return g16::skinny_launch<_Float16>(reinterpret_cast<const _Float16*>(A), B, C, bias, M, N, K, ksplit, workspace,
+                                      workspace_bytes, counters, counter_bytes, stream);
+}

@@ -1,0 +1,118 @@
+"""Kernel runtime: entry-point lookup, argument marshalling, streams and split-reduction workspaces.
+
+MI355X counterpart of the reference's NVRTC/cuLaunchKernel runtime (src/gtx16_fp16/kernels.py:253-355).
+The kernels are compiled ahead of time for gfx950 into ``libg16.so``; each reference kernel name
+maps to one C entry point of that library (``include/g16.h``) that picks its own launch shape and
+enqueues on the stream it is given. Nothing is compiled at run time.
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _clib
+
+# kernels.py:253 -- M <= 8 takes the skinny path (fp32 math on unquantised activations).
+SKINNY_MAX_M = 8
+
+# Reference kernel names (kernels.py:139-250) -> C entry points of libg16.so.
+KERNELS = {
+    "rowscale_f32": "g16_rowscale_f32",
+    "rowscale_f16": "g16_rowscale_f16",
+    "hgemm_f32out": "g16_hgemm_f32out",
+    "hgemm_f16out": "g16_hgemm_f16out",
+    "hgemm_splitk": "g16_hgemm_splitk",
+    "skinny_f32in": "g16_skinny_f32in",
+    "skinny_f16in": "g16_skinny_f16in",
+}
+
+
+def get_kernel(name: str, device: torch.device | None = None):
+    """The bound C entry point replacing reference kernel ``name`` (kernels.py:341-355). The
+    library holds code for every device it supports, so ``device`` only exists for signature
+    compatibility."""
+    del device
+    try:
+        sym = KERNELS[name]
+    except KeyError:
+        raise KeyError(f"unknown kernel {name!r}; known: {sorted(KERNELS)}") from None
+    return getattr(_clib.load(), sym)
+
+
+def stream_handle(device_index: int) -> int:
+    """Raw handle of torch's current HIP stream on ``device_index`` (kernels.py:294-296)."""
+    return torch._C._cuda_getCurrentRawStream(device_index)
+
+
+def _arg(a):
+    if isinstance(a, torch.Tensor):
+        return a.data_ptr()
+    return a
+
+
+def launch(kernel, args: list, what: str = "g16 kernel") -> None:
+    """Call a C entry point with tensors passed as device pointers and ``None`` as NULL; raise
+    ``RuntimeError`` on a nonzero status (kernels.py:299-321)."""
+    _clib.check(kernel(*[_arg(a) for a in args]), what)
+
+
+class PreparedLaunch:
+    """A bound entry point whose per-call Python work is only the ctypes call itself: for the
+    token-by-token FastLinear path (kernels.py:324-338)."""
+
+    __slots__ = ("fn", "what")
+
+    def __init__(self, fn, what: str):
+        self.fn = fn
+        self.what = what
+
+    def __call__(self, *args) -> None:
+        status = self.fn(*args)
+        if status != 0:
+            _clib.check(status, self.what)
+
+
+# ---- split-reduction buffers ----------------------------------------------------------------
+# The split-K GEMM and the skinny GEMV sum their K slices through two buffers: fp32 partials (no
+# initialisation needed) and per-tile arrival counters, which must be zero before first use and
+# which every call leaves zero again. One pair is kept per (device, stream) and grown on demand:
+# calls on one stream are ordered, so they can share it; calls on different streams get
+# different buffers.
+_ws_lock = threading.Lock()
+_partials: dict[tuple[int, int], torch.Tensor] = {}
+_counters: dict[tuple[int, int], torch.Tensor] = {}
+_MIN_PARTIAL_BYTES = 1 << 20
+_MIN_COUNTER_BYTES = 64 << 10
+
+
+def _grown(table: dict, key, nbytes: int, floor: int, device, zero: bool) -> torch.Tensor:
+    buf = table.get(key)
+    if buf is None or buf.numel() < nbytes:
+        with _ws_lock:
+            buf = table.get(key)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, floor, 0 if buf is None else 2 * buf.numel())
+                # Allocated (and zero-filled) on the current stream, so ordered before the kernels.
+                make = torch.zeros if zero else torch.empty
+                buf = make(size, dtype=torch.uint8, device=device)
+                table[key] = buf
+    return buf
+
+
+def split_buffers(device: torch.device, stream: int, partial_bytes: int, counter_bytes: int):
+    """(partials ptr, partials size, counters ptr, counters size) for a split reduction on
+    ``stream``; (0, 0, 0, 0) when the call needs none."""
+    if partial_bytes <= 0 and counter_bytes <= 0:
+        return 0, 0, 0, 0
+    key = (device.index or 0, stream)
+    part = _grown(_partials, key, partial_bytes, _MIN_PARTIAL_BYTES, device, zero=False)
+    cnt = _grown(_counters, key, counter_bytes, _MIN_COUNTER_BYTES, device, zero=True)
+    return part.data_ptr(), part.numel(), cnt.data_ptr(), cnt.numel()
+
+
+def release_workspaces() -> None:
+    """Drop every cached split-reduction buffer (they are re-created on demand)."""
+    with _ws_lock:
+        _partials.clear()
+        _counters.clear()

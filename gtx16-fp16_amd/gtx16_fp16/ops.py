@@ -1,0 +1,148 @@
+"""Host-side dispatch: support checks, path selection, launches on the current torch stream.
+
+Mirrors the reference's src/gtx16_fp16/ops.py (same names, arguments, dtype rules and fallbacks);
+the kernels behind it are the gfx950 ones of libg16.so.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _clib
+from .kernels import SKINNY_MAX_M, split_buffers, stream_handle
+
+# ops.py:14-16 -- rows whose |max| exceeds this are scaled down by a power of two before the fp16
+# cast (GEMM path); the result is scaled back in fp32.
+ROW_SCALE_THRESHOLD = 1024.0
+
+# The gfx target libg16.so is built for.
+TARGET_ARCH = "gfx950"
+
+_cus: dict[int, int] = {}
+_arch_ok: dict[int, bool] = {}
+
+
+def _dev_index(device) -> int:
+    if device is None:
+        return torch.cuda.current_device()
+    d = torch.device(device) if not isinstance(device, int) else torch.device("cuda", device)
+    return d.index if d.index is not None else torch.cuda.current_device()
+
+
+def _is_target(idx: int) -> bool:
+    ok = _arch_ok.get(idx)
+    if ok is None:
+        arch = getattr(torch.cuda.get_device_properties(idx), "gcnArchName", "") or ""
+        ok = torch.version.hip is not None and arch.split(":")[0] == TARGET_ARCH
+        _arch_ok[idx] = ok
+    return ok
+
+
+def is_affected(device: torch.device | int | None = None) -> bool:
+    """True when the device is one these kernels target: an MI355X-class gfx950 GPU.
+
+    (The reference's predicate selects Turing TU116/TU117 devices, ops.py:19-26; here it decides
+    whether ``patch`` swaps layers by default.)"""
+    if not torch.cuda.is_available():
+        return False
+    return _is_target(_dev_index(device))
+
+
+def supported(x2d: torch.Tensor, w_t: torch.Tensor) -> bool:
+    """x2d: [M, K] fp16/fp32 contiguous GPU tensor; w_t: [K, N] fp16 contiguous, 16-byte aligned;
+    K % 8 == 0 and N % 8 == 0 (ops.py:29-35). Additionally the device must be the gfx950 target
+    of libg16.so, so other GPUs take the torch fallback instead of failing to launch."""
+    K, N = w_t.shape
+    return (x2d.is_cuda and x2d.dim() == 2 and x2d.dtype in (torch.float16, torch.float32)
+            and w_t.dtype == torch.float16 and x2d.is_contiguous() and w_t.is_contiguous()
+            and x2d.shape[1] == K and K % 8 == 0 and N % 8 == 0 and w_t.data_ptr() % 16 == 0
+            and w_t.device == x2d.device and _is_target(x2d.device.index or 0))
+
+
+def _sm_count(device: torch.device) -> int:
+    """Compute units of ``device`` (cached; ops.py:38-42)."""
+    i = device.index or 0
+    if i not in _cus:
+        _cus[i] = torch.cuda.get_device_properties(i).multi_processor_count
+    return _cus[i]
+
+
+def skinny_config(N: int, K: int, sms: int) -> tuple[tuple[int, int, int], int]:
+    """Grid and K rows per workgroup of the skinny kernel for ``sms`` compute units
+    (ops.py:45-51): 512-column strips of 8 wavefronts, K split so that about one workgroup lands
+    on every CU."""
+    ksplit = _clib.load().g16_skinny_plan(1, N, K, sms)
+    rows = 0 if K == 0 else -(-(-(-K // ksplit)) // 8) * 8
+    ksplit = 1 if K == 0 else -(-K // rows)
+    return ((N + 511) // 512 * ksplit, 1, 1), rows
+
+
+def _aligned(x: torch.Tensor) -> torch.Tensor:
+    # The kernels read activations with 16-byte (rowscale) or dword (skinny) loads from a 16-byte
+    # aligned base; supported() checks the weight only, as the reference does, so a misaligned
+    # activation view is copied into a fresh allocation.
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
+def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
+         out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """out[M,N] = x2d[M,K] @ w_t[K,N] + bias[N]  (ops.py:65-108).
+
+    x2d fp16 or fp32; w_t fp16; bias fp32 (or None); out fp32 or fp16. Check supported() first.
+    M <= 8: fp32 math on the unquantised x (skinny path). M > 8: rows with |max| > 1024 are scaled
+    by a power of two, cast to fp16, multiplied on the matrix cores with fp32 accumulation and
+    scaled back; shapes with too few output tiles split K with a deterministic reduction."""
+    if out_dtype not in (torch.float32, torch.float16):
+        raise ValueError(f"out_dtype must be float32 or float16, got {out_dtype}")
+    lib = _clib.load()
+    M, K = x2d.shape
+    N = w_t.shape[1]
+    dev = x2d.device
+    stream = stream_handle(dev.index or 0)
+    cus = _sm_count(dev)
+    b = None if bias is None else bias.float().contiguous()
+    bptr = None if b is None else b.data_ptr()
+
+    x2d = _aligned(x2d)
+    if M <= SKINNY_MAX_M:  # memory-bound path, fp32 math
+        out = torch.empty(M, N, device=dev, dtype=torch.float32)
+        ksplit = lib.g16_skinny_plan(M, N, K, cus)
+        bufs = split_buffers(dev, stream, lib.g16_skinny_workspace_bytes(M, N, K, ksplit),
+                             lib.g16_skinny_counter_bytes(M, N, K, ksplit))
+        fn = lib.g16_skinny_f32in if x2d.dtype == torch.float32 else lib.g16_skinny_f16in
+        _clib.check(fn(x2d.data_ptr(), w_t.data_ptr(), out.data_ptr(), bptr, M, N, K, ksplit, *bufs, stream),
+                    "skinny GEMM")
+        return out if out_dtype == torch.float32 else out.to(out_dtype)
+
+    # GEMM path: fp16 inputs, with per-row power-of-two scaling for rows that would overflow.
+    x16 = torch.empty(M, K, device=dev, dtype=torch.float16)
+    rscale = torch.empty(M, device=dev, dtype=torch.float32)
+    rs_fn = lib.g16_rowscale_f32 if x2d.dtype == torch.float32 else lib.g16_rowscale_f16
+    _clib.check(rs_fn(x2d.data_ptr(), x16.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
+                "rowscale cast")
+
+    out = torch.empty(M, N, device=dev, dtype=out_dtype)
+    ksplit = lib.g16_hgemm_plan(M, N, K, cus)
+    if ksplit > 1:
+        # Too few output tiles to fill the GPU: split K, reduce the slices in a fixed order.
+        bufs = split_buffers(dev, stream, lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit),
+                             lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit))
+        st = lib.g16_hgemm_splitk(x16.data_ptr(), w_t.data_ptr(), out.data_ptr(),
+                                  1 if out_dtype == torch.float16 else 0, bptr, rscale.data_ptr(),
+                                  M, N, K, ksplit, *bufs, stream)
+        _clib.check(st, "split-K GEMM")
+        return out
+    fn = lib.g16_hgemm_f32out if out_dtype == torch.float32 else lib.g16_hgemm_f16out
+    _clib.check(fn(x16.data_ptr(), w_t.data_ptr(), out.data_ptr(), bptr, rscale.data_ptr(), M, N, K, stream),
+                "GEMM")
+    return out
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Drop-in for a @ b with 2-D fp16 inputs; falls back to torch.matmul when the shape is not
+    supported. Default output dtype: fp16, like torch (ops.py:111-119)."""
+    out_dtype = out_dtype or torch.float16
+    if a.dim() == 2 and b.dim() == 2 and a.dtype == b.dtype == torch.float16 and a.is_cuda:
+        a_c, b_c = a.contiguous(), b.contiguous()
+        if supported(a_c, b_c):
+            return mm_t(a_c, b_c, None, out_dtype)
+    return torch.matmul(a, b).to(out_dtype)

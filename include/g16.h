@@ -1,0 +1,124 @@
+/*
+ * g16.h -- C ABI of libg16.so, the gfx950 (MI355X) kernels behind gtx16_fp16.mm_t / matmul /
+ * FastLinear.
+ *
+ * Each entry point replaces one kernel that the reference compiles with NVRTC and launches by name
+ * through cuLaunchKernel (src/gtx16_fp16/kernels.py:282-338). Paths below are relative to the
+ * reference checkout.
+ *
+ * Conventions shared by every entry point:
+ *   - Plain device pointers and sizes; no torch types. fp16 data is passed as uint16_t bit
+ *     patterns (IEEE binary16), fp32 as float.
+ *   - The call enqueues work on `stream` (a hipStream_t; NULL = the legacy default stream) and
+ *     returns at once. It never synchronises and never allocates or frees device memory.
+ *   - Return value: 0 on success; a negative G16_E* code for an argument the library rejects
+ *     (nothing is enqueued then); a positive hipError_t if the HIP launch itself fails.
+ *     g16_strerror() names both kinds.
+ *   - Row-major, contiguous operands: x/A is [M,K], the weight w_t/B is [K,N] (N contiguous),
+ *     outputs are [M,N]. K and N must be multiples of 8 and every pointer 16-byte aligned (the
+ *     reference's supported() predicate, src/gtx16_fp16/ops.py:29-35, plus the alignment the
+ *     16-byte vector loads need). M == 0 or N == 0 is a no-op.
+ *   - Split reductions (split-K and skinny paths) take two caller-owned device buffers:
+ *       workspace -- fp32 partial sums, at least *_workspace_bytes(); needs no initialisation;
+ *       counters  -- per-tile arrival counters, at least *_counter_bytes(); must be all zero
+ *                    before the first use, and every call leaves them all zero again, so one
+ *                    zero-filled counter buffer serves any sequence of calls on one stream.
+ *     With ksplit == 1 neither is used (NULL/0 is fine). Calls that use the same buffers
+ *     concurrently (different streams) race.
+ *   - Results are deterministic: no floating-point atomics; split reductions sum partials in a
+ *     fixed order, so repeated calls return identical bits.
+ */
+#ifndef G16_H
+#define G16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define G16_ABI_VERSION 2
+
+/* Status codes (negative: rejected by the library before any launch). */
+#define G16_OK 0
+#define G16_E_SHAPE (-1)       /* negative size, or K or N not a multiple of 8 */
+#define G16_E_ALIGN (-2)       /* a pointer is not 16-byte aligned */
+#define G16_E_NULL (-3)        /* a required pointer is NULL */
+#define G16_E_WORKSPACE (-4)   /* workspace or counters missing or smaller than required */
+#define G16_E_SPLIT (-5)       /* ksplit out of range */
+#define G16_E_DTYPE (-6)       /* unknown dtype code */
+
+/* Semantic constants of the reference. */
+#define G16_SKINNY_MAX_M 8          /* src/gtx16_fp16/kernels.py:253 */
+#define G16_ROW_SCALE_THRESHOLD 1024.0f /* src/gtx16_fp16/ops.py:16 */
+
+int g16_abi_version(void);
+const char* g16_strerror(int status);
+
+/* ---------------------------------------------------------------------------------------------
+ * Row rescale + fp16 cast.
+ * Replaces rowscale_f32 / rowscale_f16 (src/gtx16_fp16/kernels.py:227-250), launched at
+ * src/gtx16_fp16/ops.py:86-90 with grid (M,1,1) -- here M is an argument.
+ * Per row i: amax = max_k |X[i,k]| (NaN ignored); S[i] = 2^ceil(log2(amax/thresh)) when
+ * amax > thresh, else 1 (+inf for an infinite row); Y[i,k] = fp16_rne(X[i,k] / S[i]).
+ * thresh must be a positive power of two (the reference uses 1024).
+ */
+int g16_rowscale_f32(const float* X, uint16_t* Y, float* S, int M, int K, float thresh,
+                     void* stream);
+int g16_rowscale_f16(const uint16_t* X, uint16_t* Y, float* S, int M, int K, float thresh,
+                     void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Tiled MFMA GEMM: C[M,N] = rscale[row] * (A16[M,K] @ B16[K,N]) + bias[N], fp32 accumulation.
+ * Replaces hgemm_f32out / hgemm_f16out (src/gtx16_fp16/kernels.py:139-142,148-151), launched at
+ * src/gtx16_fp16/ops.py:103-108. bias and rscale may be NULL (0 and 1). fp16 output rounds to
+ * nearest-even.
+ */
+int g16_hgemm_f32out(const uint16_t* A, const uint16_t* B, float* C, const float* bias,
+                     const float* rscale, int M, int N, int K, void* stream);
+int g16_hgemm_f16out(const uint16_t* A, const uint16_t* B, uint16_t* C, const float* bias,
+                     const float* rscale, int M, int N, int K, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Deterministic split-K GEMM for shapes with too few output tiles to fill the GPU.
+ * Replaces hgemm_splitk + the bias prefill _prefilled (src/gtx16_fp16/kernels.py:143-147,
+ * src/gtx16_fp16/ops.py:54-62,92-101). Instead of fp32 atomics into a prefilled C, each K slice
+ * writes an fp32 partial tile to the workspace; the last slice to finish a tile sums the partials
+ * in slice order, then applies rscale and bias and writes C (fp32, or fp16 when c_is_f16 != 0,
+ * so no separate cast pass). ksplit in [1, 256]; ksplit == 1 needs no workspace.
+ * g16_hgemm_plan() returns the ksplit this library would choose (1 = the plain GEMM).
+ */
+int g16_hgemm_splitk(const uint16_t* A, const uint16_t* B, void* C, int c_is_f16,
+                     const float* bias, const float* rscale, int M, int N, int K, int ksplit,
+                     void* workspace, size_t workspace_bytes, uint32_t* counters,
+                     size_t counter_bytes, void* stream);
+size_t g16_hgemm_splitk_workspace_bytes(int M, int N, int K, int ksplit);
+size_t g16_hgemm_splitk_counter_bytes(int M, int N, int K, int ksplit);
+int g16_hgemm_plan(int M, int N, int K, int num_cus);
+
+/* ---------------------------------------------------------------------------------------------
+ * Skinny GEMM (GEMV-like) for 1 <= M <= 8: C[M,N] = A[M,K] @ B16[K,N] + bias, fp32 math on the
+ * UNQUANTISED activations (fp32 or fp16), fp32 output.
+ * Replaces skinny_f32in / skinny_f16in (src/gtx16_fp16/kernels.py:212-219) and its launch
+ * configuration skinny_config (src/gtx16_fp16/ops.py:45-51,78-84; src/gtx16_fp16/linear.py:49-64).
+ * A is read with 16-byte alignment (A must be 16-byte aligned, like B).
+ * The kernel streams B once with 16-byte loads; K is split over ksplit workgroups per 512-column
+ * strip and reduced deterministically (last arriving workgroup, slice order). C needs no zero-fill.
+ * g16_skinny_plan() returns the ksplit this library would choose for num_cus compute units.
+ */
+int g16_skinny_f32in(const float* A, const uint16_t* B, float* C, const float* bias, int M, int N,
+                     int K, int ksplit, void* workspace, size_t workspace_bytes, uint32_t* counters,
+                     size_t counter_bytes, void* stream);
+int g16_skinny_f16in(const uint16_t* A, const uint16_t* B, float* C, const float* bias, int M,
+                     int N, int K, int ksplit, void* workspace, size_t workspace_bytes,
+                     uint32_t* counters, size_t counter_bytes, void* stream);
+size_t g16_skinny_workspace_bytes(int M, int N, int K, int ksplit);
+size_t g16_skinny_counter_bytes(int M, int N, int K, int ksplit);
+int g16_skinny_plan(int M, int N, int K, int num_cus);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* G16_H */

@@ -1,0 +1,336 @@
+"""GPU parity: the gfx950 kernels (through the C ABI of libg16.so) against the fp64 oracle.
+
+Bars (per the north star): rowscale exponents and fp16 casts bit-exact; relative Frobenius error
+<= 1e-3 on the GEMM paths (fp32 and fp16 output) and <= 1e-5 on the skinny fp32-accumulate path;
+split reductions bitwise repeatable. Inputs are seeded on the CPU and copied to the device, so
+the oracle sees the same bits. Shapes follow the reference's acceptance sweep
+(tests/test_correctness.py:14-18) plus the BASELINE configurations.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _inputs import outlier_rows, randn
+
+pytestmark = pytest.mark.gpu
+
+GEMM_TOL = 1e-3
+SKINNY_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def g(cuda):
+    import gtx16_fp16
+
+    return gtx16_fp16
+
+
+@pytest.fixture(scope="module")
+def lib(cuda):
+    from gtx16_fp16 import _clib
+
+    return _clib.load()
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def _stream(dev) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _split_bufs(partial_bytes: int, counter_bytes: int, dev):
+    ws = torch.empty(max(partial_bytes, 16), dtype=torch.uint8, device=dev)
+    cnt = torch.zeros(max(counter_bytes, 16), dtype=torch.uint8, device=dev)
+    return ws, cnt
+
+
+# ---------------------------------------------------------------------------------------------
+# rowscale cast: exponents and fp16 values bit-exact
+# ---------------------------------------------------------------------------------------------
+
+def _rowscale_gpu(lib, x: torch.Tensor):
+    M, K = x.shape
+    y = torch.empty(M, K, dtype=torch.float16, device=x.device)
+    s = torch.empty(M, dtype=torch.float32, device=x.device)
+    fn = lib.g16_rowscale_f32 if x.dtype == torch.float32 else lib.g16_rowscale_f16
+    st = fn(x.data_ptr(), y.data_ptr(), s.data_ptr(), M, K, 1024.0, _stream(x.device))
+    assert st == 0, st
+    torch.cuda.synchronize()
+    return y, s
+
+
+KAT_AMAX = [0.0, 1.0, 1023.9999, 1024.0, float(np.nextafter(np.float32(1024), np.float32(2048))), 2048.0,
+            float(np.nextafter(np.float32(2048), np.float32(4096))), 65504.0, 179940.0, 2e5, 3.0e38]
+
+
+@pytest.mark.parametrize("K", [8, 136, 1032, 3072, 4096, 8200])
+def test_rowscale_f32_bitexact(lib, cuda, K):
+    M = len(KAT_AMAX) + 20
+    x = randn((M, K), seed=K)
+    for i, a in enumerate(KAT_AMAX):  # row i has |max| exactly a (at a column that depends on i)
+        x[i] = x[i].clamp(-0.5, 0.5)
+        x[i, (7 * i) % K] = -a if i % 2 else a
+    x[len(KAT_AMAX) + 1, 3 % K] = float("nan")  # NaN is ignored by the max
+    x[len(KAT_AMAX) + 2, 0] = -0.0  # signed zeros keep their sign through the scaling
+    x[len(KAT_AMAX) + 2, K - 1] = 5000.0
+    x[5, (K // 2) & ~1] = -0.0
+    y, s = _rowscale_gpu(lib, x.to(cuda))
+    y_ref, s_ref, e_ref = oracle.rowscale(_np(x))
+    _assert_bits_equal(_np(s).view(np.uint32), s_ref.view(np.uint32), _np(x), "S")
+    _assert_bits_equal(_np(y).view(np.uint16), y_ref.view(np.uint16), _np(x), "Y")
+
+
+def _assert_bits_equal(got: np.ndarray, ref: np.ndarray, x: np.ndarray, what: str) -> None:
+    bad = np.argwhere(got != ref)
+    if bad.size:
+        show = []
+        for idx in bad[:8]:
+            idx = tuple(int(i) for i in idx)
+            xin = x[idx] if x.ndim == len(idx) else x[idx[0]]
+            show.append(f"{idx}: got {got[idx]:#x} ref {ref[idx]:#x} x={xin!r}")
+        raise AssertionError(f"{what}: {len(bad)} bit mismatches; first: " + "; ".join(show))
+
+
+@pytest.mark.parametrize("K", [64, 1032, 4096, 6144])
+def test_rowscale_f16_bitexact(lib, cuda, K):
+    M = 40
+    x = randn((M, K), seed=K + 1)
+    x[:, 5] = 60000.0
+    x[3, 9] = -50000.0
+    x[7] = x[7] * 1e-6  # values that go subnormal in fp16 after scaling
+    x[7, 0] = 2000.0
+    x16 = x.half()
+    x16[9, 3] = -0.0
+    assert (x16 == 0).any()  # row 7 holds fp16 zeros of both signs and subnormals
+    y, s = _rowscale_gpu(lib, x16.to(cuda))
+    y_ref, s_ref, _ = oracle.rowscale(_np(x16))
+    _assert_bits_equal(_np(s).view(np.uint32), s_ref.view(np.uint32), _np(x16), "S")
+    _assert_bits_equal(_np(y).view(np.uint16), y_ref.view(np.uint16), _np(x16), "Y")
+
+
+def test_rowscale_infinite_row_is_nonfinite(g, cuda):
+    x = randn((16, 256), seed=5)
+    x[2, 10] = float("inf")
+    w = randn((256, 64), seed=6, scale=0.1, dtype=torch.float16)
+    y = g.mm_t(x.to(cuda), w.to(cuda), None, torch.float32)
+    torch.cuda.synchronize()
+    assert not torch.isfinite(y[2]).any()
+    assert torch.isfinite(torch.cat([y[:2], y[3:]])).all()
+
+
+# ---------------------------------------------------------------------------------------------
+# GEMM path (M > 8) through mm_t: plain tiles and split-K
+# ---------------------------------------------------------------------------------------------
+
+SHAPES = [  # (M, K, N) -- reference sweep, tests/test_correctness.py:14-18
+    (128, 128, 128), (256, 512, 384), (1000, 1032, 776), (129, 136, 8), (3, 4096, 4096),
+    (1, 1024, 3072), (8, 2048, 520), (9, 64, 64), (4096, 4096, 1024), (17, 8, 4104),
+    (64, 1024, 1024), (33, 4096, 768), (200, 1032, 136),
+]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES)
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_mm_t_matches_oracle(g, cuda, M, K, N, out_dtype, with_bias):
+    x = randn((M, K), seed=M * 7 + K * 3 + N, scale=0.5, dtype=torch.float16)
+    w = randn((K, N), seed=M + K + N, scale=0.5, dtype=torch.float16)
+    b = randn((N,), seed=N + 11) if with_bias else None
+    xd, wd = x.to(cuda), w.to(cuda)
+    bd = b.to(cuda) if b is not None else None
+    assert g.supported(xd, wd)
+    y = g.mm_t(xd, wd, bd, out_dtype)
+    torch.cuda.synchronize()
+    assert y.dtype == out_dtype and y.shape == (M, N)
+    assert torch.isfinite(y).all()
+    ref = oracle.mm_t(_np(x), _np(w), None if b is None else _np(b), "float32")
+    tol = SKINNY_TOL if (M <= 8 and out_dtype == torch.float32) else GEMM_TOL
+    assert oracle.rel_err(_np(y.float()), ref) <= tol
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (1024, 1024, 1024), (65536 // 64, 768, 3072)])
+def test_large_gemm_fp32_activations_with_outliers(g, cuda, M, K, N):
+    # C4: fp32 activations, 1% of rows with |max| ~ U[2e3, 2e5], fp16 weights ~ N(0, 0.02^2)
+    x = outlier_rows(randn((M, K), seed=0), 0.01, 2e3, 2e5, seed=3)
+    w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16)
+    y = g.mm_t(x.to(cuda), w.to(cuda), None, torch.float32)
+    torch.cuda.synchronize()
+    xs = _np(x)
+    y16, S, e = oracle.rowscale(xs)
+    assert (e > 0).sum() == int(round(0.01 * M))
+    ref = oracle.gemm(y16, S, _np(w), None, "float32")
+    assert oracle.rel_err(_np(y), ref) <= GEMM_TOL
+
+
+def test_constant_16_known_answer(g, cuda):
+    # tests/test_correctness.py:103-109: 16*16 summed over K = 4096 is exactly 1,048,576.
+    x = torch.full((128, 4096), 16.0, device=cuda).half()
+    w = torch.full((4096, 128), 16.0, device=cuda).half()
+    y = g.mm_t(x, w, None, torch.float32)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    assert torch.equal(y, torch.full_like(y, 16 * 16 * 4096))
+
+
+@pytest.mark.parametrize("M", [1, 5, 64, 300])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.float16])
+def test_massive_activations(g, cuda, M, in_dtype):
+    # tests/test_correctness.py:112-126
+    K, N = 3072, 1024
+    x = randn((M, K), seed=1)
+    x[:, 7] = 179940.0 if in_dtype == torch.float32 else 60000.0
+    x[0, 100] = -120000.0 if in_dtype == torch.float32 else -50000.0
+    x = x.to(in_dtype)
+    w = randn((K, N), seed=2, scale=0.3, dtype=torch.float16)
+    y = g.mm_t(x.to(cuda), w.to(cuda), None, torch.float32)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    ref = oracle.mm_t(_np(x), _np(w), None, "float32")
+    tol = SKINNY_TOL if M <= 8 else GEMM_TOL
+    assert oracle.rel_err(_np(y), ref) <= tol
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 1024, 1024), (64, 4096, 1024), (1024, 1024, 1024), (33, 4096, 768)])
+def test_splitk_deterministic_and_matches_plain(lib, cuda, M, K, N):
+    a = randn((M, K), seed=0, dtype=torch.float16).to(cuda)
+    b = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
+    bias = randn((N,), seed=2, scale=0.02).to(cuda)
+    s = torch.ones(M, device=cuda)
+    st = _stream(cuda)
+    plain = torch.empty(M, N, device=cuda)
+    assert lib.g16_hgemm_f32out(a.data_ptr(), b.data_ptr(), plain.data_ptr(), bias.data_ptr(), s.data_ptr(),
+                                M, N, K, st) == 0
+    ref = oracle.gemm(_np(a), _np(s), _np(b), _np(bias), "float32")
+    for ksplit in (2, 3, 8, 16):
+        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit),
+                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit), cuda)
+        outs = []
+        for _ in range(10):
+            c = torch.empty(M, N, device=cuda)
+            assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c.data_ptr(), 0, bias.data_ptr(), s.data_ptr(),
+                                        M, N, K, ksplit, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(),
+                                        st) == 0
+            outs.append(c)
+        torch.cuda.synchronize()
+        for o in outs[1:]:
+            assert torch.equal(o, outs[0])
+        # (the ten calls share one counter buffer: each relies on the previous one leaving it zero,
+        # or no slice would see itself arrive last and C would stay unwritten)
+        assert oracle.rel_err(_np(outs[0]), ref) <= GEMM_TOL
+        assert int(cnt.view(torch.int32).abs().sum().item()) == 0
+    assert oracle.rel_err(_np(plain), ref) <= GEMM_TOL
+
+
+def test_splitk_fp16_output(lib, cuda):
+    M, K, N = 64, 4096, 1024
+    a = randn((M, K), seed=0, dtype=torch.float16).to(cuda)
+    b = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
+    bias = randn((N,), seed=2, scale=0.02).to(cuda)
+    s = torch.ones(M, device=cuda)
+    ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 8),
+                          lib.g16_hgemm_splitk_counter_bytes(M, N, K, 8), cuda)
+    c = torch.empty(M, N, dtype=torch.float16, device=cuda)
+    assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c.data_ptr(), 1, bias.data_ptr(), s.data_ptr(),
+                                M, N, K, 8, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(),
+                                _stream(cuda)) == 0
+    torch.cuda.synchronize()
+    ref = oracle.gemm(_np(a), _np(s), _np(b), _np(bias), "float32")
+    assert oracle.rel_err(_np(c.float()), ref) <= GEMM_TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# skinny path (M <= 8)
+# ---------------------------------------------------------------------------------------------
+
+SKINNY_SHAPES = [(1, 4096, 4096), (4, 4096, 4096), (1, 1024, 3072), (8, 2048, 520), (3, 4096, 4096),
+                 (2, 8, 8), (5, 200, 72), (7, 1032, 776), (6, 64, 4104)]
+
+
+@pytest.mark.parametrize("M,K,N", SKINNY_SHAPES)
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_skinny_matches_oracle(g, cuda, M, K, N, x_dtype, with_bias):
+    x = randn((M, K), seed=M + K, dtype=x_dtype)
+    w = randn((K, N), seed=K + N, scale=0.02, dtype=torch.float16)
+    b = randn((N,), seed=N, scale=0.02) if with_bias else None
+    y = g.mm_t(x.to(cuda), w.to(cuda), None if b is None else b.to(cuda), torch.float32)
+    torch.cuda.synchronize()
+    ref = oracle.skinny(_np(x), _np(w), None if b is None else _np(b))
+    assert oracle.rel_err(_np(y), ref) <= SKINNY_TOL
+
+
+@pytest.mark.parametrize("ksplit", [1, 2, 5, 16, 64])
+def test_skinny_explicit_splits_deterministic(lib, cuda, ksplit):
+    M, K, N = 4, 4096, 4096
+    x = randn((M, K), seed=0).to(cuda)
+    w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
+    b = randn((N,), seed=2, scale=0.02).to(cuda)
+    ws, cnt = _split_bufs(lib.g16_skinny_workspace_bytes(M, N, K, ksplit),
+                          lib.g16_skinny_counter_bytes(M, N, K, ksplit), cuda)
+    outs = []
+    for _ in range(5):
+        c = torch.full((M, N), float("nan"), device=cuda)
+        assert lib.g16_skinny_f32in(x.data_ptr(), w.data_ptr(), c.data_ptr(), b.data_ptr(), M, N, K, ksplit,
+                                    ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), _stream(cuda)) == 0
+        outs.append(c)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ref = oracle.skinny(_np(x), _np(w), _np(b))
+    assert oracle.rel_err(_np(outs[0]), ref) <= SKINNY_TOL
+
+
+def test_skinny_M1_4096_cache_rotation_parity(g, cuda):
+    # The benchmark rotates distinct weight copies; every copy must give the oracle's answer.
+    K = N = 4096
+    x = randn((1, K), seed=0)
+    b = randn((N,), seed=2, scale=0.02)
+    for seed in (1, 101):
+        w = randn((K, N), seed=seed, scale=0.02, dtype=torch.float16)
+        y = g.mm_t(x.to(cuda), w.to(cuda), b.to(cuda), torch.float32)
+        torch.cuda.synchronize()
+        assert oracle.rel_err(_np(y), oracle.skinny(_np(x), _np(w), _np(b))) <= SKINNY_TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# C ABI argument checks (rejected before any launch)
+# ---------------------------------------------------------------------------------------------
+
+def test_abi_rejects_bad_arguments(lib, cuda):
+    a = torch.zeros(64, 64, dtype=torch.float16, device=cuda)
+    c = torch.zeros(64, 64, device=cuda)
+    st = _stream(cuda)
+    assert lib.g16_hgemm_f32out(a.data_ptr(), a.data_ptr(), c.data_ptr(), None, None, 64, 64, 60, st) == -1
+    assert lib.g16_hgemm_f32out(a.data_ptr() + 2, a.data_ptr(), c.data_ptr(), None, None, 64, 64, 64, st) == -2
+    assert lib.g16_hgemm_f32out(None, a.data_ptr(), c.data_ptr(), None, None, 64, 64, 64, st) == -3
+    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 1024, 4,
+                                None, 0, None, 0, st) == -4
+    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 1024, 4,
+                                c.data_ptr(), c.numel() * 4, None, 0, st) == -4
+    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 64, 0,
+                                None, 0, None, 0, st) == -5
+    assert lib.g16_skinny_f32in(a.data_ptr(), a.data_ptr(), c.data_ptr(), None, 9, 64, 64, 1, None, 0, None, 0,
+                                st) == -1
+    assert lib.g16_rowscale_f32(a.data_ptr(), a.data_ptr(), c.data_ptr(), 4, 64, 1000.0, st) == -1
+    assert lib.g16_hgemm_f32out(a.data_ptr(), a.data_ptr(), c.data_ptr(), None, None, 0, 64, 64, st) == 0
+    assert b"workspace" in lib.g16_strerror(-4)
+
+
+def test_mixed_shapes_share_split_buffers(g, cuda):
+    # Skinny and split-K calls of different shapes on one stream share the cached partial and
+    # counter buffers; every result must still match the oracle (regression: counters once lived
+    # inside the partials buffer, where another shape's partial sums could land on them).
+    shapes = [(1, 4096, 4096), (64, 1024, 1024), (4, 1024, 3072), (64, 4096, 1024), (8, 2048, 520),
+              (33, 4096, 768), (1, 4096, 4096)]
+    for i, (M, K, N) in enumerate(shapes * 2):
+        x = randn((M, K), seed=100 + i)
+        w = randn((K, N), seed=200 + i, scale=0.05, dtype=torch.float16)
+        y = g.mm_t(x.to(cuda), w.to(cuda), None, torch.float32)
+        torch.cuda.synchronize()
+        ref = oracle.mm_t(_np(x), _np(w), None, "float32")
+        assert oracle.rel_err(_np(y), ref) <= (SKINNY_TOL if M <= 8 else GEMM_TOL), (M, K, N)
