@@ -10,70 +10,101 @@
 //   * 256 threads = 4 wavefronts per workgroup; a workgroup owns a BM x BN output tile, each
 //     wavefront a (BM/WGM) x (BN/WGN) sub-tile made of 32x32 blocks computed with
 //     v_mfma_f32_32x32x16_f16 (fp32 accumulators).
-//   * K advances in steps of BK = 64 through a two-stage LDS ring: the global loads for step k+1
-//     are issued before the MFMAs of step k and land in the other stage after them, one barrier
-//     per step.
-//   * MFMA operands need K-contiguous runs per lane for both A and B. A tiles are copied as is
-//     ([row][k]); B tiles ([k][n] in memory) are transposed in registers while staging (each
-//     thread loads KR rows x 8 columns and writes 8 runs of KR halves), so LDS holds [n][k].
-//   * LDS rows are 64 halves (128 bytes, 8 chunks of 16 bytes); chunk c of row r is stored at
-//     chunk c ^ swizzle(r), which keeps the 16-byte fragment reads and the staging writes free of
-//     bank conflicts.
+//   * K advances in steps of BK = 64 through a two-stage LDS ring filled by DMA
+//     (buffer_load_dwordx4 ... lds): the loads for step k+1 are issued before the MFMAs of step
+//     k and never pass through registers; one barrier per step. Lanes whose 16-byte chunk lies
+//     outside the matrix (ragged M, N, K or a split-K slice boundary) are given an out-of-range
+//     buffer offset, which makes the DMA write zeros.
+//   * The DMA writes 1 KB per wavefront instruction (lane i -> bytes 16i..16i+15), so the LDS
+//     layout is chosen through which global chunk each lane fetches: A is stored [row][k] with
+//     16-byte chunk c of row r at chunk c ^ (r & 7); B is stored [k][n] like the weight, chunk c of
+//     row k at chunk c ^ 2(k & 3). Both keep the fragment reads below free of bank conflicts.
+//   * MFMA operands need K-contiguous runs per lane. A fragments are one 16-byte LDS read each.
+//     B fragments use the gfx950 transposing read ds_read_b64_tr_b16: within each 16-lane group,
+//     lane p receives element p%4 of the 8-byte pieces addressed by lanes p/4 + 4j (j = 0..3), so
+//     pointing lane q at B[k0 + q/4][n0 + 4(q%4)] hands lane p the run B[k0..k0+3][n0 + p]; two
+//     such reads give the 8-deep run one operand needs.
+//   * Fragments are double-buffered in registers: the reads for k-substep s+1 are issued before
+//     the MFMAs of substep s.
 //   * Tiles are assigned XCD-aware: the hardware deals workgroups round-robin over the 8 XCDs, so
 //     workgroup b is mapped to tile (b % 8) * (T / 8) + b / 8, giving each XCD a contiguous run
 //     of tiles, which a grouped (GROUP_M rows at a time) order turns into a compact 2-D block
 //     that shares A rows and B columns in that XCD's L2.
 //   * Split-K: slice z of tile t covers K range [z*kchunk, (z+1)*kchunk). Every slice stores its
 //     fp32 accumulators to the workspace in the lanes' own register order (fully coalesced 16-byte
-//     stores); the last slice to arrive adds all slices in slice order and runs the epilogue.
-//     Deterministic, and bias/scale/cast are fused (the reference prefills C with the bias and
-//     adds with fp32 atomics, kernels.py:119-122, ops.py:54-62).
+//     device-coherent stores); the last slice to arrive adds all slices in slice order and runs the
+//     epilogue. Deterministic, and bias/scale/cast are fused (the reference prefills C with the bias
+//     and adds with fp32 atomics, kernels.py:119-122, ops.py:54-62).
 #include "g16_common.hpp"
 
 namespace g16 {
 namespace {
 
 constexpr int BK = 64;
-constexpr int kThreads = 256;
 constexpr int kGroupM = 8;
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every descriptor's range: reads 0
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
+// Generic -> LDS address-space pointer (the transpose-read builtin takes one).
+__device__ inline lds_short4v* as_lds4(const unsigned char* p) { return (lds_short4v*)(p); }
+
+// 16-byte DMA global -> LDS: lane i's chunk at buffer offset `off` lands at LDS byte lds + 16 i.
+// Issued as inline asm so the compiler's wait-counter bookkeeping does not see an LDS write it
+// cannot tell apart from the stage being read (it would wait for the DMA before every LDS
+// read); the kernel waits for its DMA explicitly (vmcnt 0) before the barrier that publishes a
+// stage. Vector memory returns in order, so the compiler's own vmcnt waits stay correct (they can
+// only wait longer) with these loads in flight.
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, const unsigned char* lds, uint32_t off) {
+  const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(off), "s"(rsrc)
+               : "memory", "m0");
+}
+__device__ inline void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <int BM_, int BN_, int WGM_, int WGN_>
 struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
-  static_assert(WGM * WGN == 4, "4 wavefronts per workgroup");
+  static constexpr int WAVES = WGM * WGN;
+  static constexpr int THREADS = WAVES * kWave;
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;  // wavefront sub-tile
   static constexpr int TM = WTM / 32, TN = WTN / 32;      // 32x32 MFMA blocks per wavefront
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 blocks");
-  static constexpr int A_CH = BM * BK / 8 / kThreads;  // 16-byte A chunks per thread
-  static constexpr int KR = BK * BN / (kThreads * 8);   // B rows per thread (8 columns each)
-  static_assert(A_CH >= 1 && (KR == 2 || KR == 4 || KR == 8), "staging shape");
-  static constexpr int NB = BN / 8;  // 8-column groups per B row
-  static constexpr int LDS_HALVES = 2 * (BM + BN) * BK;
+  static constexpr int A_BYTES = BM * BK * 2;            // one stage of A
+  static constexpr int B_BYTES = BK * BN * 2;            // one stage of B
+  static constexpr int A_INSTR = A_BYTES / 1024 / WAVES;  // 1 KB DMA instructions per wavefront
+  static constexpr int B_INSTR = B_BYTES / 1024 / WAVES;
+  static constexpr int B_ROW_CHUNKS = BN / 8;            // 16-byte chunks per B row
+  static constexpr int B_ROWS_PER_INSTR = 64 / B_ROW_CHUNKS;
+  static_assert(A_INSTR >= 1 && B_INSTR >= 1 && B_ROW_CHUNKS >= 8 && B_ROW_CHUNKS <= 64, "staging shape");
 };
 
-using Cfg256 = TileCfg<256, 256, 2, 2>;
+using Cfg256 = TileCfg<256, 256, 2, 4>;  // 8 wavefronts: two per SIMD
 using Cfg128 = TileCfg<128, 128, 2, 2>;
 using Cfg64 = TileCfg<64, 128, 1, 4>;
 using Cfg32 = TileCfg<32, 128, 1, 4>;
 
 __device__ inline int swz_a(int row) { return row & 7; }
-__device__ inline int swz_b(int n) { return (n & 7) ^ ((n >> 3) & 7); }
-
-// Halves (hi16 of one dword, lo16 of another) packers for the B transpose.
-__device__ inline uint32_t pick(uint32_t lo_src, uint32_t hi_src, bool odd) {
-  return odd ? ((lo_src >> 16) | (hi_src & 0xffff0000u)) : ((lo_src & 0xffffu) | (hi_src << 16));
-}
+__device__ inline int swz_b(int k) { return (k & 3) << 1; }
 
 template <class Cfg, bool OUT_F16, bool SPLITK>
-__global__ __launch_bounds__(kThreads) void hgemm_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+__global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
                                                          void* __restrict__ Cv, const float* __restrict__ bias,
                                                          const float* __restrict__ rscale, float* __restrict__ part,
                                                          uint32_t* __restrict__ counters, int M, int N, int K,
                                                          int kchunk, int ksplit, int ntm, int ntn) {
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN, KR = Cfg::KR, NB = Cfg::NB;
-  __shared__ __attribute__((aligned(16))) _Float16 smem[Cfg::LDS_HALVES];
-  _Float16* const As = smem;                 // [2][BM][BK]
-  _Float16* const Bs = smem + 2 * BM * BK;   // [2][BN][BK]
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN;
+  // Two LDS stages as distinct objects, indexed only by compile-time stage numbers, so the
+  // compiler can tell the DMA into one stage from the fragment reads of the other (it would
+  // otherwise wait for the DMA before every read).
+  __shared__ __attribute__((aligned(1024))) unsigned char sA0[Cfg::A_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char sA1[Cfg::A_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB0[Cfg::B_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB1[Cfg::B_BYTES];
 
   // ---- tile assignment (XCD-aware, grouped) ----
   const int ntiles = ntm * ntn;
@@ -91,62 +122,62 @@ __global__ __launch_bounds__(kThreads) void hgemm_kernel(const _Float16* __restr
   const int kend = min(K, kbeg + kchunk);
   const int nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm0 = (wave / Cfg::WGN) * Cfg::WTM;
   const int wn0 = (wave % Cfg::WGN) * Cfg::WTN;
 
-  // ---- global -> register staging ----
-  u32x4 ra[Cfg::A_CH];
-  u32x4 rb[KR];
-  const int a_c = tid & 7;    // 16-byte chunk within the 64-half row
-  const int a_r = tid >> 3;   // rows a_r + 32*i
-  const int b_nb = tid % NB;  // 8-column group
-  const int b_kb = tid / NB;  // rows b_kb*KR .. +KR-1
+  // ---- DMA staging: per-lane chunk assignment (independent of k) ----
+  // A: instruction i of this wavefront fills LDS rows a_row0 + 8i; lane -> (row, logical chunk)
+  const int a_row0 = wave * Cfg::A_INSTR * 8 + (lane >> 3);
+  // B: instruction i fills rows b_row0 + i * B_ROWS_PER_INSTR
+  const int b_row0 = wave * Cfg::B_INSTR * Cfg::B_ROWS_PER_INSTR + lane / Cfg::B_ROW_CHUNKS;
+  const int b_phys = lane % Cfg::B_ROW_CHUNKS;
 
-  auto gload = [&](int k0) {
+  auto dma = [&](unsigned char* as, unsigned char* bs, int k0) {
+    // A rows m0 + row, columns k0 + 8c; the descriptor is rebased at (m0, k0).
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A) + static_cast<size_t>(m0) * K + k0, 0, 0x7fffffff,
+                                          kRawBufferDword3);
 #pragma unroll
-    for (int i = 0; i < Cfg::A_CH; ++i) {
-      const int row = m0 + a_r + 32 * i;
-      const int kk = k0 + a_c * 8;
-      ra[i] = (row < M && kk < kend) ? *reinterpret_cast<const u32x4*>(A + static_cast<size_t>(row) * K + kk)
-                                     : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < Cfg::A_INSTR; ++i) {
+      const int row = a_row0 + i * 8;
+      const int c = (lane & 7) ^ swz_a(row);
+      const bool ok = (m0 + row < M) && (k0 + c * 8 < kend);
+      const uint32_t off = ok ? static_cast<uint32_t>((row * K + c * 8) * 2) : kOob;
+      dma16(ra, as + (wave * Cfg::A_INSTR + i) * 1024, off);
     }
-    const int col = n0 + b_nb * 8;
+    // B rows k0 + row, columns n0 + 8c; rebased at (k0, n0).
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B) + static_cast<size_t>(k0) * N + n0, 0, 0x7fffffff,
+                                          kRawBufferDword3);
 #pragma unroll
-    for (int j = 0; j < KR; ++j) {
-      const int kr = k0 + b_kb * KR + j;
-      rb[j] = (kr < kend && col < N) ? *reinterpret_cast<const u32x4*>(B + static_cast<size_t>(kr) * N + col)
-                                     : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < Cfg::B_INSTR; ++i) {
+      const int row = b_row0 + i * Cfg::B_ROWS_PER_INSTR;
+      const int c = b_phys ^ swz_b(row);
+      const bool ok = (k0 + row < kend) && (n0 + c * 8 < N);
+      const uint32_t off = ok ? static_cast<uint32_t>((row * N + c * 8) * 2) : kOob;
+      dma16(rb, bs + (wave * Cfg::B_INSTR + i) * 1024, off);
     }
   };
 
-  auto swrite = [&](int stage) {
-    _Float16* as = As + stage * BM * BK;
-    _Float16* bs = Bs + stage * BN * BK;
-#pragma unroll
-    for (int i = 0; i < Cfg::A_CH; ++i) {
-      const int row = a_r + 32 * i;
-      *reinterpret_cast<u32x4*>(as + row * BK + ((a_c ^ swz_a(row)) * 8)) = ra[i];
-    }
-    const int kl = b_kb * KR;
-    const int chunk = kl / 8, sub = kl % 8;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      const int nl = b_nb * 8 + n;
-      _Float16* dst = bs + nl * BK + ((chunk ^ swz_b(nl)) * 8) + sub;
-      const int dw = n >> 1;
-      const bool odd = (n & 1) != 0;
-      uint32_t w[KR / 2];
-#pragma unroll
-      for (int p = 0; p < KR / 2; ++p) w[p] = pick(rb[2 * p][dw], rb[2 * p + 1][dw], odd);
-      if constexpr (KR == 8) {
-        *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
-      } else if constexpr (KR == 4) {
-        *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = w[0];
-      }
-    }
+  // ---- fragment addressing (byte offsets within a stage) ----
+  const int frow = lane & 31;  // A fragment row within a 32-block
+  const int fk = lane >> 5;    // which 8-run of the 16-wide K step
+  // B transposed reads: 16-lane group g covers columns +16*(g&1), k rows +8*(g>>1); lane q of the
+  // group addresses row q/4, columns 4*(q%4).
+  const int bg = lane >> 4, bq = lane & 15;
+  const int b_col_in = 16 * (bg & 1) + 4 * (bq & 3);  // column within the 32-block
+  const int b_k_in = 8 * (bg >> 1) + (bq >> 2);       // k row within the 16-step (first read)
+
+  auto a_off = [&](int i, int ks) {
+    const int row = wm0 + 32 * i + frow;
+    const int chunk = ks * 2 + fk;
+    return row * (BK * 2) + ((chunk ^ swz_a(row)) * 16);
+  };
+  auto b_off = [&](int j, int krow) {
+    const int col = wn0 + 32 * j + b_col_in;
+    return krow * (BN * 2) + (((col >> 3) ^ swz_b(krow)) * 16) + (col & 7) * 2;
   };
 
   float16v acc[TM][TN];
@@ -155,40 +186,53 @@ __global__ __launch_bounds__(kThreads) void hgemm_kernel(const _Float16* __restr
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
 
-  const int frow = lane & 31;  // fragment row (A) / column (B) within a 32-block
-  const int fk = lane >> 5;    // which 8-run of the 16-wide K step
+  half8 af[2][TM], bf[2][TN];
+  auto read_frags = [&](int buf, const unsigned char* as, const unsigned char* bs, int ks) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[buf][i] = *reinterpret_cast<const half8*>(as + a_off(i, ks));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int krow = ks * 16 + b_k_in;
+      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(as_lds4(bs + b_off(j, krow)));
+      const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(as_lds4(bs + b_off(j, krow + 4)));
+      bf[buf][j] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
 
-  if (nk > 0) {
-    gload(kbeg);
-    swrite(0);
-  }
-  __syncthreads();
-  for (int it = 0; it < nk; ++it) {
-    const int cur = it & 1;
-    if (it + 1 < nk) gload(kbeg + (it + 1) * BK);
-    const _Float16* as = As + cur * BM * BK;
-    const _Float16* bs = Bs + cur * BN * BK;
+  // One K step on the stage (as, bs); DMA of the next step into (an, bn) when `more`.
+  auto step = [&](const unsigned char* as, const unsigned char* bs, unsigned char* an, unsigned char* bn, bool more,
+                  int knext) {
+    if (more) dma(an, bn, knext);
+    read_frags(0, as, bs, 0);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      const int chunk = ks * 2 + fk;
-      half8 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = wm0 + 32 * i + frow;
-        af[i] = *reinterpret_cast<const half8*>(as + row * BK + ((chunk ^ swz_a(row)) * 8));
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = wn0 + 32 * j + frow;
-        bf[j] = *reinterpret_cast<const half8*>(bs + n * BK + ((chunk ^ swz_b(n)) * 8));
-      }
+      if (ks + 1 < BK / 16) read_frags((ks + 1) & 1, as, bs, ks + 1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks & 1][i], bf[ks & 1][j], acc[i][j], 0, 0, 0);
+      if (ks + 1 < BK / 16) {
+        // Interleave: the next substep's LDS reads go between this substep's MFMAs.
+        constexpr int kReads = TM + 2 * TN;
+#pragma unroll
+        for (int r = 0; r < kReads; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN > kReads ? TM * TN - kReads : 0, 0);
+      }
     }
-    if (it + 1 < nk) swrite(cur ^ 1);
+    wait_dma();  // this wavefront's DMA for the next step has landed
     __syncthreads();
+  };
+
+  if (nk > 0) dma(sA0, sB0, kbeg);
+  wait_dma();
+  __syncthreads();
+  for (int it = 0; it < nk; it += 2) {
+    step(sA0, sB0, sA1, sB1, it + 1 < nk, kbeg + (it + 1) * BK);
+    if (it + 1 < nk) step(sA1, sB1, sA0, sB0, it + 2 < nk, kbeg + (it + 2) * BK);
   }
 
   // ---- split-K: publish this slice, let the last slice reduce ----
@@ -357,7 +401,8 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
     counters = counters_in;
     part = static_cast<float*>(ws);
   }
-  const dim3 grid(static_cast<unsigned>(p.ntm * p.ntn), static_cast<unsigned>(ks.ksplit)), block(kThreads);
+  const dim3 grid(static_cast<unsigned>(p.ntm * p.ntn), static_cast<unsigned>(ks.ksplit)),
+      block(p.tile == Tile::T256 ? Cfg256::THREADS : 256);
   const auto* a = reinterpret_cast<const _Float16*>(A);
   const auto* b = reinterpret_cast<const _Float16*>(B);
   hipStream_t s = static_cast<hipStream_t>(stream);

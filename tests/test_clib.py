@@ -1,0 +1,87 @@
+"""CPU tests of libg16.so's C ABI: it loads, exports every function include/g16.h declares, and
+rejects bad arguments before any launch (so these calls need no GPU)."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+
+from gtx16_fp16 import _clib, kernels
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "g16.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(g16_\w+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _clib.load()
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == set(_clib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_strerror(lib):
+    assert lib.g16_abi_version() == _clib.ABI_VERSION
+    assert b"aligned" in lib.g16_strerror(-2)
+    assert b"workspace" in lib.g16_strerror(-4)
+    assert lib.g16_strerror(-99) == b"unknown g16 status"
+
+
+def test_argument_errors_need_no_gpu(lib):
+    A = 0x1000  # never dereferenced: every call below is rejected before a launch
+    assert lib.g16_hgemm_f32out(A, A, A, None, None, 64, 64, 60, None) == -1      # K % 8
+    assert lib.g16_hgemm_f32out(A, A, A, None, None, 64, 60, 64, None) == -1      # N % 8
+    assert lib.g16_hgemm_f32out(A + 2, A, A, None, None, 64, 64, 64, None) == -2  # alignment
+    assert lib.g16_hgemm_f32out(None, A, A, None, None, 64, 64, 64, None) == -3   # NULL
+    assert lib.g16_hgemm_f32out(A, A, A, None, None, 0, 64, 64, None) == 0        # M == 0: no-op
+    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, 64, 64, 1024, 4, None, 0, None, 0, None) == -4
+    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, 64, 64, 1024, 0, None, 0, None, 0, None) == -5
+    assert lib.g16_skinny_f32in(A, A, A, None, 9, 64, 64, 1, None, 0, None, 0, None) == -1   # M > 8
+    assert lib.g16_skinny_f32in(A, A, A, None, 4, 4096, 4096, 8, A, 1 << 30, None, 0, None) == -4
+    assert lib.g16_rowscale_f32(A, A, A, 4, 64, 1000.0, None) == -1               # threshold not 2^k
+    assert lib.g16_rowscale_f32(A, A, A, 4, 64, -1024.0, None) == -1
+
+
+def test_plans_and_buffer_sizes(lib):
+    assert lib.g16_skinny_plan(1, 4096, 4096, 256) >= 8
+    assert lib.g16_hgemm_plan(4096, 4096, 4096, 256) == 1           # enough tiles: no split
+    assert lib.g16_hgemm_plan(64, 1024, 4096, 256) > 1              # few tiles: split K
+    ks = lib.g16_skinny_plan(4, 4096, 4096, 256)
+    assert lib.g16_skinny_workspace_bytes(4, 4096, 4096, ks) == ks * 4 * 4096 * 4
+    assert lib.g16_skinny_counter_bytes(4, 4096, 4096, ks) == (4096 // 512) * 256
+    assert lib.g16_skinny_workspace_bytes(4, 4096, 4096, 1) == 0
+    assert lib.g16_hgemm_splitk_workspace_bytes(64, 1024, 1024, 1) == 0
+    assert lib.g16_hgemm_splitk_counter_bytes(64, 1024, 1024, 4) > 0
+
+
+def test_nonzero_status_raises_runtime_error():
+    # kernels.py:299-302 convention: a failed launch raises RuntimeError naming the status
+    with pytest.raises(RuntimeError, match="status 98"):
+        kernels.launch(lambda *a: 98, [1, 2], "fake kernel")
+    with pytest.raises(RuntimeError, match="skinny"):
+        kernels.PreparedLaunch(lambda *a: -4, "skinny GEMM")(1, 2)
+    kernels.PreparedLaunch(lambda *a: 0, "ok")()
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="missing"):
+        _clib.load(tmp_path / "libg16.so")
+
+
+def test_get_kernel_names_match_reference_kernels():
+    assert set(kernels.KERNELS) == {"rowscale_f32", "rowscale_f16", "hgemm_f32out", "hgemm_f16out",
+                                    "hgemm_splitk", "skinny_f32in", "skinny_f16in"}
+    assert kernels.get_kernel("hgemm_f32out") is not None
+    with pytest.raises(KeyError):
+        kernels.get_kernel("hgemm")

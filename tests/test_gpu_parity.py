@@ -334,3 +334,31 @@ def test_mixed_shapes_share_split_buffers(g, cuda):
         torch.cuda.synchronize()
         ref = oracle.mm_t(_np(x), _np(w), None, "float32")
         assert oracle.rel_err(_np(y), ref) <= (SKINNY_TOL if M <= 8 else GEMM_TOL), (M, K, N)
+
+
+# ---------------------------------------------------------------------------------------------
+# committed golden fixtures (hand-derived exponents, exact rational results)
+# ---------------------------------------------------------------------------------------------
+
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+def test_golden_rowscale_known_answers(lib, cuda):
+    kat = np.load(GOLDEN / "rowscale_kat.npz")
+    x = torch.from_numpy(kat["x"]).to(cuda)
+    y, s = _rowscale_gpu(lib, x)
+    assert np.array_equal(_np(s).view(np.uint32), kat["S"].view(np.uint32))
+    y_ref, _, _ = oracle.rowscale(kat["x"])
+    _assert_bits_equal(_np(y).view(np.uint16), y_ref.view(np.uint16), kat["x"], "Y")
+
+
+@pytest.mark.parametrize("name", ["skinny_m3", "skinny_m8", "gemm_m12", "gemm_m9"])
+def test_golden_mm_t_exact(g, cuda, name):
+    d = np.load(GOLDEN / "mm_t_exact.npz")
+    x, w = d[f"{name}_x"], d[f"{name}_w"]
+    b = d[f"{name}_b"] if f"{name}_b" in d.files else None
+    y = g.mm_t(torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda),
+               None if b is None else torch.from_numpy(b).to(cuda), torch.float32)
+    torch.cuda.synchronize()
+    tol = SKINNY_TOL if x.shape[0] <= 8 else GEMM_TOL
+    assert oracle.rel_err(_np(y), d[f"{name}_out"]) <= tol
