@@ -49,6 +49,10 @@ def parse(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--report", type=str, default=None, help="also write per-kernel details to this JSON file")
+    ap.add_argument("--only", choices=["gemm", "rowscale", "skinny", "copy"], default=None,
+                    help="launch just this kernel --steps times on the headline shapes (for rocprofv3 counter "
+                         "runs) and print its average time; copy = a plain 256 MiB device copy, the "
+                         "calibration for FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args(argv)
 
 
@@ -216,6 +220,62 @@ def cpu_baseline(torch) -> dict:
     }
 
 
+def run_only(torch, lib, what: str, steps: int, dev) -> dict:
+    """Back-to-back launches of one kernel, for profiling runs."""
+    from _inputs import outlier_rows, randn
+
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if what == "copy":
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        fn = lambda: dst.copy_(src)  # noqa: E731
+        bytes_moved = 2 * n
+    elif what == "skinny":
+        M, K, N = 1, 4096, 4096
+        x = randn((M, K), seed=0).to(dev)
+        b = randn((N,), seed=2, scale=0.02).to(dev)
+        ws = [randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(dev) for _ in range(16)]
+        out = torch.empty(M, N, device=dev)
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        ks = lib.g16_skinny_plan(M, N, K, cus)
+        part = torch.empty(max(lib.g16_skinny_workspace_bytes(M, N, K, ks), 256), dtype=torch.uint8, device=dev)
+        cnt = torch.zeros(max(lib.g16_skinny_counter_bytes(M, N, K, ks), 256), dtype=torch.uint8, device=dev)
+        it = iter(range(1 << 30))
+
+        def fn():
+            w = ws[next(it) % 16]
+            lib.g16_skinny_f32in(x.data_ptr(), w.data_ptr(), out.data_ptr(), b.data_ptr(), M, N, K, ks,
+                                 part.data_ptr(), part.numel(), cnt.data_ptr(), cnt.numel(), stream)
+        bytes_moved = M * K * 4 + K * N * 2 + N * 4 + M * N * 4
+    else:
+        M = K = N = 4096
+        x = outlier_rows(randn((M, K), seed=0), 0.01, 2e3, 2e5, seed=3).to(dev)
+        x16 = torch.empty(M, K, dtype=torch.float16, device=dev)
+        rs = torch.empty(M, device=dev)
+        lib.g16_rowscale_f32(x.data_ptr(), x16.data_ptr(), rs.data_ptr(), M, K, 1024.0, stream)
+        if what == "rowscale":
+            fn = lambda: lib.g16_rowscale_f32(x.data_ptr(), x16.data_ptr(), rs.data_ptr(), M, K, 1024.0,  # noqa: E731
+                                              stream)
+            bytes_moved = M * K * 6 + M * 4
+        else:
+            w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(dev)
+            out = torch.empty(M, N, device=dev)
+            fn = lambda: lib.g16_hgemm_f32out(x16.data_ptr(), w.data_ptr(), out.data_ptr(), None,  # noqa: E731
+                                              rs.data_ptr(), M, N, K, stream)
+            bytes_moved = None
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ms = event_time_ms(fn, steps, torch)
+    res = {"only": what, "steps": steps, "avg_ms": round(ms, 5)}
+    if bytes_moved:
+        res["GB/s"] = round(bytes_moved / (ms * 1e-3) / 1e9, 1)
+    else:
+        res["TFLOP/s"] = round(2.0 * 4096 ** 3 / (ms * 1e-3) / 1e12, 1)
+    return res
+
+
 def main(argv=None) -> int:
     args = parse(argv)
     if args.gpus != 1:
@@ -233,6 +293,9 @@ def main(argv=None) -> int:
     lib = _clib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.only:
+        print(json.dumps(run_only(torch, lib, args.only, args.steps, dev)), flush=True)
+        return 0
     c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev)
     sk = bench_skinny(torch, lib, g, args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch)
