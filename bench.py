@@ -38,6 +38,7 @@ for _p in (str(REPO), str(REPO / "gtx16-fp16_amd"), str(REPO / "tests")):
         sys.path.insert(0, _p)
 
 MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 flop/clk/CU (dense fp16)
+TRAFFIC_FILE = REPO / "profiles" / "traffic.json"  # FETCH_SIZE/WRITE_SIZE runs (calibrated), per launch
 HBM_PEAK_GBS = 8000.0
 METRIC = "TFLOPS (% MFMA peak) at 4096^3; GB/s (% HBM peak) for M=1 4096x4096 mm_t"
 
@@ -49,6 +50,9 @@ def parse(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--report", type=str, default=None, help="also write per-kernel details to this JSON file")
+    ap.add_argument("--all", action="store_true",
+                    help="also time every BASELINE configuration through the public API and write the per-config "
+                         "table to --report (default gpurun_out/configs.json); the JSON line is unchanged")
     ap.add_argument("--only", choices=["gemm", "rowscale", "skinny", "copy"], default=None,
                     help="launch just this kernel --steps times on the headline shapes (for rocprofv3 counter "
                          "runs) and print its average time; copy = a plain 256 MiB device copy, the "
@@ -194,6 +198,64 @@ def bench_skinny(torch, lib, g, steps: int, warmup: int, dev, copies: int = 16) 
     }
 
 
+def _time_call(torch, fn, steps: int, warmup: int = 3) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    return min(event_time_ms(fn, steps, torch) for _ in range(3))
+
+
+def bench_all(torch, g, steps: int, dev) -> list:
+    """Every BASELINE configuration through the public API (algorithmic units: flops = 2MNK,
+    bytes = M*K*sizeof(x) + 2*K*N + 4*N*[bias] + M*N*sizeof(out))."""
+    from _inputs import outlier_rows, randn
+
+    rows = []
+
+    def add(name, M, K, N, xbytes, obytes, bias, ms, extra=None):
+        flop = 2.0 * M * N * K
+        nbytes = M * K * xbytes + 2 * K * N + (4 * N if bias else 0) + M * N * obytes
+        r = {"config": name, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2),
+             "TFLOPS": round(flop / (ms * 1e-3) / 1e12, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+             "pct_mfma_peak": round(100 * flop / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 2),
+             "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+        if extra:
+            r.update(extra)
+        rows.append(r)
+        print(json.dumps(r), flush=True)
+
+    # C1: matmul 1024^3, fp16 in/out
+    a = randn((1024, 1024), seed=0, dtype=torch.float16).to(dev)
+    b = randn((1024, 1024), seed=1, dtype=torch.float16).to(dev)
+    add("C1 matmul fp16 1024^3", 1024, 1024, 1024, 2, 2, False, _time_call(torch, lambda: g.matmul(a, b), steps))
+    # C2: skinny decode (fp32 x, fp16 w_t, fp32 bias, fp32 out), weights rotated over 16 copies
+    for (M, K, N) in ((1, 4096, 4096), (4, 4096, 4096), (1, 1024, 3072)):
+        x = randn((M, K), seed=0).to(dev)
+        w0 = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(dev)
+        copies = max(16, (512 << 20) // (K * N * 2))
+        ws = [w0.clone() for _ in range(copies)]
+        bias = randn((N,), seed=2, scale=0.02).to(dev)
+        idx = iter(range(1 << 30))
+        ms = _time_call(torch, lambda: g.mm_t(x, ws[next(idx) % copies], bias, torch.float32), max(steps, copies))
+        add(f"C2 skinny {M}x{K}x{N}", M, K, N, 4, 4, True, ms, {"weight_copies": copies, "timing": "per mm_t call"})
+        del ws
+    # C3: split-K (fp16 A, fp32 out + bias); repeat runs must be bitwise equal
+    for (M, K, N) in ((64, 1024, 1024), (64, 4096, 1024)):
+        x = randn((M, K), seed=0, dtype=torch.float16).to(dev)
+        w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(dev)
+        bias = randn((N,), seed=2, scale=0.02).to(dev)
+        outs = [g.mm_t(x, w, bias, torch.float32) for _ in range(10)]
+        same = all(torch.equal(o, outs[0]) for o in outs[1:])
+        ms = _time_call(torch, lambda: g.mm_t(x, w, bias, torch.float32), steps)
+        add(f"C3 split-K {M}x{K}x{N}", M, K, N, 2, 4, True, ms, {"repeat_bitwise_equal": same})
+    # C4: 4096^3 fp32 activations with outlier rows, fp32 out
+    x = outlier_rows(randn((4096, 4096), seed=0), 0.01, 2e3, 2e5, seed=3).to(dev)
+    w = randn((4096, 4096), seed=1, scale=0.02, dtype=torch.float16).to(dev)
+    add("C4 mm_t 4096^3 fp32 x", 4096, 4096, 4096, 4, 4, False,
+        _time_call(torch, lambda: g.mm_t(x, w, None, torch.float32), steps))
+    return rows
+
+
 def cpu_baseline(torch) -> dict:
     """The reference's CPU path: torch fp32 matmul (ops.py:119 fallback) at 4096^3 on the host."""
     from _inputs import outlier_rows, randn
@@ -276,6 +338,15 @@ def run_only(torch, lib, what: str, steps: int, dev) -> dict:
     return res
 
 
+def traffic_bytes(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+    (scaled by a plain copy's readings), or None when they are not there."""
+    try:
+        return int(json.loads(TRAFFIC_FILE.read_text())[kernel]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main(argv=None) -> int:
     args = parse(argv)
     if args.gpus != 1:
@@ -296,6 +367,7 @@ def main(argv=None) -> int:
     if args.only:
         print(json.dumps(run_only(torch, lib, args.only, args.steps, dev)), flush=True)
         return 0
+    configs = bench_all(torch, g, args.steps, dev) if args.all else None
     c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev)
     sk = bench_skinny(torch, lib, g, args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch)
@@ -324,11 +396,12 @@ def main(argv=None) -> int:
             "peak": MFMA_F16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / MFMA_F16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes("gemm"),
             "kernel_ms": round(c4["gemm_kernel_ms"], 5),
         },
         "rowscale_kernel": {"ms": round(c4["rowscale_kernel_ms"], 5), "GB/s": round(c4["rowscale_kernel_gbs"], 1),
-                            "frac_hbm": round(c4["rowscale_kernel_gbs"] / HBM_PEAK_GBS, 4)},
+                            "frac_hbm": round(c4["rowscale_kernel_gbs"] / HBM_PEAK_GBS, 4),
+                            "traffic": traffic_bytes("rowscale")},
         "skinny_m1": {
             "workload": "mm_t M=1 K=N=4096, fp32 x, fp16 w_t, fp32 bias, fp32 out (16 rotated weight copies)",
             "value": round(sk["kernel_gbs"], 1),
@@ -341,7 +414,7 @@ def main(argv=None) -> int:
                 "peak": HBM_PEAK_GBS,
                 "unit": "GB/s",
                 "frac": round(sk["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                "traffic": None,
+                "traffic": traffic_bytes("skinny"),
                 "kernel_us": round(sk["kernel_us"], 3),
             },
             "bytes_per_launch": sk["bytes_per_launch"],
@@ -350,8 +423,10 @@ def main(argv=None) -> int:
         },
         "cpu_baseline": cpu,
     }
-    if args.report:
-        Path(args.report).write_text(json.dumps({"c4": c4, "skinny_m1": sk, "cpu": cpu}, indent=2))
+    report = args.report or ("gpurun_out/configs.json" if args.all else None)
+    if report:
+        Path(report).parent.mkdir(parents=True, exist_ok=True)
+        Path(report).write_text(json.dumps({"c4": c4, "skinny_m1": sk, "cpu": cpu, "configs": configs}, indent=2))
     print(json.dumps(line), flush=True)
     return 0
 

@@ -86,7 +86,7 @@ struct TileCfg {
                 "every wavefront issues the same number of DMA instructions");
   static_assert(B_ROW_CHUNKS >= 16 && B_ROW_CHUNKS <= 64, "B swizzle needs >= 16 chunks per row");
   static constexpr int DMA_PER_STEP = A_INSTR + B_INSTR;  // per wavefront
-  static_assert(NSTAGE >= 2 && (NSTAGE - 2) * DMA_PER_STEP <= 63, "vmcnt range");
+  static_assert(NSTAGE >= 3 && (NSTAGE - 2) * DMA_PER_STEP <= 63, "vmcnt range");
 };
 
 using Cfg256 = TileCfg<256, 256, 32, 2, 4, 4>;  // 8 wavefronts (two per SIMD), 4-stage ring, 128 KB
@@ -233,31 +233,34 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
   };
 
-  // Ring of NSTAGE stages. During step j: MFMAs of step j (registers), LDS reads of step j+1,
-  // DMA of step j+NSTAGE-1 into the stage step j-1 used (freed by the barrier that ended step
-  // j-1). Before the barrier ending step j, step j+2 must have landed: it is read during j+1.
+  // Ring of NSTAGE stages. During step j: MFMAs of step j (its fragments are already in
+  // registers, read during step j-1), LDS reads of step j+1, and DMA of step j+NSTAGE into stage
+  // j%NSTAGE -- the stage step j came from, which nobody reads any more. Before the barrier that
+  // ends step j, step j+2 must have landed (it is read during j+1): NSTAGE-2 younger steps of DMA
+  // may still be in flight, giving each DMA NSTAGE-1 steps to arrive.
   // The three streams are cut into PARTS slices issued round-robin (DMA, MFMAs, LDS reads), so no
   // wavefront front-loads its DMA and the memory pipes see a steady trickle between barriers.
-  constexpr int AHEAD = NSTAGE - 1;
-  constexpr int LAG = NSTAGE - 3;  // DMA steps allowed in flight at the barrier
+  constexpr int LAG = NSTAGE - 2;
   static_assert(NSTAGE >= 3, "three stages at least");
   constexpr int NMFMA = KS * TM * TN, NFRAG = KS * (TM + TN), NDMA = Cfg::DMA_PER_STEP;
   constexpr int PARTS = NDMA;
   if (nk > 0) {
 #pragma unroll
-    for (int s = 0; s < AHEAD; ++s) dma(s, kbeg + s * BK);
+    for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
   }
   wait_dma_le<LAG * NDMA>();  // steps 0 and 1 have landed
   __syncthreads();
   if (nk > 0) read_frags(0, 0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __syncthreads();  // every wavefront holds step 0 in registers: stage 0 may be refilled
   for (int it = 0; it < nk; it += 2) {
     // two steps per trip so the fragment buffer index is a compile-time constant
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int j = it + h;
       if (j < nk) {
-        const int kd = kbeg + (j + AHEAD) * BK;
-        const int std_ = (j + AHEAD) % NSTAGE, stf = (j + 1) % NSTAGE;
+        const int kd = kbeg + (j + NSTAGE) * BK;
+        const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
         const bool next = j + 1 < nk;
         const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b(kd);
 #pragma unroll
@@ -273,7 +276,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
           __builtin_amdgcn_sched_barrier(0);
         }
         wait_dma_le<LAG * NDMA>();  // step j+2 has landed (this wavefront's part)
-        __syncthreads();            // ... every wavefront's part; stage j is free
+        __syncthreads();            // ... every wavefront's part; step j+1 is in registers
       }
     }
   }
