@@ -10,8 +10,8 @@ for M=1 4096x4096 mm_t":
   fp16 weights, fp32 out: one step = one mm_t call (rowscale cast + MFMA GEMM), inputs resident in
   HBM, ``steps`` calls timed between two ``torch.cuda.synchronize()``.
 * ``roofline`` -- the GEMM kernel alone (the dominant kernel): 2*M*N*K flop per launch divided by
-  its average launch duration from HIP events around ``steps`` back-to-back launches on the
-  stream the kernel runs on, against the fp16 dense MFMA peak.
+  its average launch duration, from a HIP event pair around each GEMM launch of ``steps``
+  (rowscale, GEMM) sequences on the stream the kernels run on, against the fp16 dense MFMA peak.
 * ``skinny_m1`` -- the second half of the metric: GB/s of the M=1 K=N=4096 skinny path, kernel
   time from HIP events around a captured HIP graph of launches that rotate over 16 distinct 32 MiB
   weight copies (512 MiB, twice the 256 MB Infinity Cache, so bytes come from HBM), against the
@@ -57,6 +57,8 @@ def parse(argv=None):
                     help="launch just this kernel --steps times on the headline shapes (for rocprofv3 counter "
                          "runs) and print its average time; copy = a plain 256 MiB device copy, the "
                          "calibration for FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--bert", action="store_true",
+                    help="time only the BERT-base configuration (fp32 vs patch()) and print its JSON line")
     return ap.parse_args(argv)
 
 
@@ -111,11 +113,23 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev) -> dict:
     def gemm():
         lib.g16_hgemm_f32out(x16.data_ptr(), w.data_ptr(), out.data_ptr(), None, rs.data_ptr(), M, N, K, stream)
 
-    rowscale()
+    # The same launch sequence as a timed step (rowscale, then GEMM), with an event pair around
+    # every GEMM launch, so the GEMM's average duration is taken over dispatches in the same state
+    # as those of the timed steps (every GEMM dispatch of this run follows a rowscale pass).
     for _ in range(warmup):
+        rowscale()
         gemm()
     torch.cuda.synchronize()
-    gemm_ms = min(event_time_ms(gemm, steps, torch) for _ in range(3))
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for b, c in evs:
+        rowscale()
+        b.record()
+        gemm()
+        c.record()
+    torch.cuda.synchronize()
+    gemm_ms = statistics.fmean(b.elapsed_time(c) for b, c in evs)
+    # rowscale alone is short enough that an event pair around each launch inflates it by a few
+    # microseconds: its figure comes from back-to-back launches instead.
     rowscale_ms = min(event_time_ms(rowscale, steps, torch) for _ in range(3))
     tflops = flop / (wall_ms * 1e-3) / 1e12
     gemm_tflops = flop / (gemm_ms * 1e-3) / 1e12
@@ -253,7 +267,48 @@ def bench_all(torch, g, steps: int, dev) -> list:
     w = randn((4096, 4096), seed=1, scale=0.02, dtype=torch.float16).to(dev)
     add("C4 mm_t 4096^3 fp32 x", 4096, 4096, 4096, 4, 4, False,
         _time_call(torch, lambda: g.mm_t(x, w, None, torch.float32), steps))
+    del x, w
+    rows.append(bench_bert(torch, g, dev))
+    print(json.dumps(rows[-1]), flush=True)
     return rows
+
+
+def bench_bert(torch, g, dev, reps: int = 3) -> dict:
+    """C5: random-init BERT-base, 256 x 256 token ids, fp32 forward, then patch() and again; tokens/s
+    of each and the cosine of the mean-pooled (and CLS) embeddings."""
+    import torch.nn.functional as F
+    from _models import BERT_LINEARS, bert_base, embeddings, token_ids
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    model = bert_base(seed=0).to(dev)
+    ids = token_ids(256, 256, seed=0).to(dev)
+
+    def timed():
+        emb = embeddings(model, ids)  # warm-up
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(reps):
+            emb = embeddings(model, ids)
+        torch.cuda.synchronize()
+        return emb, (time.perf_counter() - t) / reps
+
+    ref, t32 = timed()
+    n = g.patch(model)
+    torch.cuda.empty_cache()
+    out, t16 = timed()
+    cos = [F.cosine_similarity(o.double(), r.double(), dim=1) for o, r in zip(out, ref)]
+    tokens = ids.numel()
+    # Linear work per forward: 12 layers x (4 x 768^2 + 2 x 768 x 3072) MACs per token, plus the pooler.
+    lin_flop = 2.0 * tokens * 12 * (4 * 768 * 768 + 2 * 768 * 3072) + 2.0 * 256 * 768 * 768
+    del model
+    torch.cuda.empty_cache()
+    return {"config": "C5 BERT-base patch, 256x256 tokens, fp32 activations", "linears_patched": n,
+            "linears_expected": BERT_LINEARS, "tokens_per_s": round(tokens / t16, 1),
+            "fp32_tokens_per_s": round(tokens / t32, 1), "speedup_vs_fp32": round(t32 / t16, 3),
+            "ms_per_forward": round(t16 * 1e3, 2), "fp32_ms_per_forward": round(t32 * 1e3, 2),
+            "linear_TFLOPS_equiv": round(lin_flop / t16 / 1e12, 1),
+            "cosine_mean_pooled_min": round(cos[0].min().item(), 8),
+            "cosine_cls_min": round(cos[1].min().item(), 8)}
 
 
 def cpu_baseline(torch) -> dict:
@@ -366,6 +421,9 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
     if args.only:
         print(json.dumps(run_only(torch, lib, args.only, args.steps, dev)), flush=True)
+        return 0
+    if args.bert:
+        print(json.dumps(bench_bert(torch, g, dev)), flush=True)
         return 0
     configs = bench_all(torch, g, args.steps, dev) if args.all else None
     c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev)
