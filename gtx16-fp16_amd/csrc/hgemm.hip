@@ -7,25 +7,27 @@
 // cast (K contiguous), B the fp16 weight w_t (N contiguous).
 //
 // Structure:
-//   * 256 threads = 4 wavefronts per workgroup; a workgroup owns a BM x BN output tile, each
-//     wavefront a (BM/WGM) x (BN/WGN) sub-tile made of 32x32 blocks computed with
-//     v_mfma_f32_32x32x16_f16 (fp32 accumulators).
-//   * K advances in steps of BK = 64 through a two-stage LDS ring filled by DMA
-//     (buffer_load_dwordx4 ... lds): the loads for step k+1 are issued before the MFMAs of step
-//     k and never pass through registers; one barrier per step. Lanes whose 16-byte chunk lies
-//     outside the matrix (ragged M, N, K or a split-K slice boundary) are given an out-of-range
-//     buffer offset, which makes the DMA write zeros.
+//   * A workgroup owns a BM x BN output tile; each wavefront owns a (BM/WGM) x (BN/WGN) sub-tile
+//     made of 32x32 blocks computed with v_mfma_f32_32x32x16_f16 (fp32 accumulators). The large
+//     tile is 256x256 with 8 wavefronts (two per SIMD); smaller tiles (128x128, 64x128, 32x128)
+//     use 4 wavefronts and serve small M and split-K.
+//   * K advances in steps of BK through a ring of NSTAGE LDS stages filled by DMA
+//     (buffer_load_dwordx4 ... lds), so operand tiles never pass through registers. Lanes whose
+//     16-byte chunk lies outside the matrix (ragged M, N, K or a split-K slice boundary) are given
+//     an out-of-range buffer offset, which makes the DMA write zeros.
 //   * The DMA writes 1 KB per wavefront instruction (lane i -> bytes 16i..16i+15), so the LDS
-//     layout is chosen through which global chunk each lane fetches: A is stored [row][k] with
-//     16-byte chunk c of row r at chunk c ^ (r & 7); B is stored [k][n] like the weight, chunk c of
-//     row k at chunk c ^ 2(k & 3). Both keep the fragment reads below free of bank conflicts.
+//     layout is chosen through which global chunk each lane fetches: A is stored [row][k], B
+//     [k][n] like the weight, each with a 16-byte-chunk XOR swizzle (swz_a, swz_b) that keeps the
+//     fragment reads free of bank conflicts.
 //   * MFMA operands need K-contiguous runs per lane. A fragments are one 16-byte LDS read each.
 //     B fragments use the gfx950 transposing read ds_read_b64_tr_b16: within each 16-lane group,
 //     lane p receives element p%4 of the 8-byte pieces addressed by lanes p/4 + 4j (j = 0..3), so
 //     pointing lane q at B[k0 + q/4][n0 + 4(q%4)] hands lane p the run B[k0..k0+3][n0 + p]; two
 //     such reads give the 8-deep run one operand needs.
-//   * Fragments are double-buffered in registers: the reads for k-substep s+1 are issued before
-//     the MFMAs of substep s.
+//   * Schedules: the 8-wavefront tile runs a ping-pong between the two wavefronts of each SIMD
+//     (one issues a step's MFMAs while the other reads LDS and issues DMA, swapping at every
+//     barrier); the 4-wavefront tiles interleave DMA, MFMAs and the next step's fragment reads
+//     (fragments double-buffered in registers) with one barrier per step.
 //   * Tiles are assigned XCD-aware: the hardware deals workgroups round-robin over the 8 XCDs, so
 //     workgroup b is mapped to tile (b % 8) * (T / 8) + b / 8, giving each XCD a contiguous run
 //     of tiles, which a grouped (GROUP_M rows at a time) order turns into a compact 2-D block
@@ -109,6 +111,11 @@ template <int N>
 __device__ inline void wait_dma_le() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+
+// Workgroup barrier without the counter waits __syncthreads() adds: the caller has already waited
+// for exactly the memory operations the next phase depends on. The memory clobber keeps the
+// compiler from moving LDS accesses across it.
+__device__ inline void phase_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <class Cfg, bool OUT_F16, bool SPLITK>
 __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
@@ -233,50 +240,91 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
   };
 
-  // Ring of NSTAGE stages. During step j: MFMAs of step j (its fragments are already in
-  // registers, read during step j-1), LDS reads of step j+1, and DMA of step j+NSTAGE into stage
-  // j%NSTAGE -- the stage step j came from, which nobody reads any more. Before the barrier that
-  // ends step j, step j+2 must have landed (it is read during j+1): NSTAGE-2 younger steps of DMA
-  // may still be in flight, giving each DMA NSTAGE-1 steps to arrive.
-  // The three streams are cut into PARTS slices issued round-robin (DMA, MFMAs, LDS reads), so no
-  // wavefront front-loads its DMA and the memory pipes see a steady trickle between barriers.
-  constexpr int LAG = NSTAGE - 2;
   static_assert(NSTAGE >= 3, "three stages at least");
   constexpr int NMFMA = KS * TM * TN, NFRAG = KS * (TM + TN), NDMA = Cfg::DMA_PER_STEP;
-  constexpr int PARTS = NDMA;
-  if (nk > 0) {
+  if constexpr (Cfg::WAVES == 8 && !SPLITK) {
+    // Ping-pong schedule for two wavefronts per SIMD. Wavefronts 0-3 (group 0) and 4-7 (group 1)
+    // land one of each on every SIMD. Each wavefront alternates a memory phase M_j (fragment reads
+    // of step j from LDS, DMA of step j+D into the ring) and a compute phase C_j (the 16 MFMAs of
+    // step j), with a workgroup barrier after every phase; group 1 starts one phase late, so on
+    // every SIMD one wavefront streams MFMAs while the other one waits on memory.
+    //   Ring hazards, with D = NSTAGE - 1: the DMA issued in M_j writes stage (j+D)%NSTAGE, which
+    // last held step j-1; both groups read step j-1 in M_{j-1}, which ends at or before the barrier
+    // that opens M_j for either group. The fragment reads of M_j need every wavefront's DMA of
+    // step j: each wavefront waits for its own at the end of M_{j-1}, and the barrier after that
+    // phase publishes it to the group that reads next.
+    constexpr int D = NSTAGE - 1;
+    const int grp = wave >> 2;
+    if (nk > 0) {
 #pragma unroll
-    for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
-  }
-  wait_dma_le<LAG * NDMA>();  // steps 0 and 1 have landed
-  __syncthreads();
-  if (nk > 0) read_frags(0, 0);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __syncthreads();  // every wavefront holds step 0 in registers: stage 0 may be refilled
-  for (int it = 0; it < nk; it += 2) {
-    // two steps per trip so the fragment buffer index is a compile-time constant
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = it + h;
-      if (j < nk) {
-        const int kd = kbeg + (j + NSTAGE) * BK;
-        const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
-        const bool next = j + 1 < nk;
+      for (int s = 0; s < D; ++s) dma(s, kbeg + s * BK);
+    }
+    wait_dma_le<(D - 1) * NDMA>();  // step 0 has landed
+    phase_barrier();
+    if (grp == 1) phase_barrier();
+    for (int j = 0; j < nk; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(0, j % NSTAGE);
+      {
+        const int kd = kbeg + (j + D) * BK;
         const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b(kd);
 #pragma unroll
-        for (int p = 0; p < PARTS; ++p) {
-          dma_op(std_, kd, ra, rb, p);
-          __builtin_amdgcn_sched_barrier(0);
+        for (int d = 0; d < NDMA; ++d) dma_op((j + D) % NSTAGE, kd, ra, rb, d);
+      }
+      wait_dma_le<(D - 1) * NDMA>();  // step j+1 has landed (this wavefront's part)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // step j's fragments are in registers
+      phase_barrier();
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(h, m);
-          if (next) {
+      for (int m = 0; m < NMFMA; ++m) mfma_op(0, m);
+      __builtin_amdgcn_sched_barrier(0);
+      phase_barrier();
+    }
+    if (grp == 0) phase_barrier();  // every wavefront passes the same number of barriers
+  } else {
+    // Ring of NSTAGE stages. During step j: MFMAs of step j (its fragments are already in
+    // registers, read during step j-1), LDS reads of step j+1, and DMA of step j+NSTAGE into
+    // stage j%NSTAGE -- the stage step j came from, which nobody reads any more. Before the
+    // barrier that ends step j, step j+2 must have landed (it is read during j+1): NSTAGE-2
+    // younger steps of DMA may still be in flight, giving each DMA NSTAGE-1 steps to arrive.
+    // The three streams are cut into PARTS slices issued round-robin (DMA, MFMAs, LDS reads), so
+    // no wavefront front-loads its DMA and the memory pipes see a steady trickle between barriers.
+    constexpr int LAG = NSTAGE - 2;
+    constexpr int PARTS = NDMA;
+    if (nk > 0) {
 #pragma unroll
-            for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(h ^ 1, stf, f);
+      for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
+    }
+    wait_dma_le<LAG * NDMA>();  // steps 0 and 1 have landed
+    __syncthreads();
+    if (nk > 0) read_frags(0, 0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();  // every wavefront holds step 0 in registers: stage 0 may be refilled
+    for (int it = 0; it < nk; it += 2) {
+      // two steps per trip so the fragment buffer index is a compile-time constant
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = it + h;
+        if (j < nk) {
+          const int kd = kbeg + (j + NSTAGE) * BK;
+          const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
+          const bool next = j + 1 < nk;
+          const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b(kd);
+#pragma unroll
+          for (int p = 0; p < PARTS; ++p) {
+            dma_op(std_, kd, ra, rb, p);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(h, m);
+            if (next) {
+#pragma unroll
+              for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(h ^ 1, stf, f);
+            }
+            __builtin_amdgcn_sched_barrier(0);
           }
-          __builtin_amdgcn_sched_barrier(0);
+          wait_dma_le<LAG * NDMA>();  // step j+2 has landed (this wavefront's part)
+          __syncthreads();            // ... every wavefront's part; step j+1 is in registers
         }
-        wait_dma_le<LAG * NDMA>();  // step j+2 has landed (this wavefront's part)
-        __syncthreads();            // ... every wavefront's part; step j+1 is in registers
       }
     }
   }
