@@ -117,7 +117,7 @@ __device__ inline void wait_dma_le() {
 // compiler from moving LDS accesses across it.
 __device__ inline void phase_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <class Cfg, bool OUT_F16, bool SPLITK>
+template <class Cfg, bool OUT_F16, bool SPLITK, bool PACKED_A = false>
 __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
                                                          void* __restrict__ Cv, const float* __restrict__ bias,
                                                          const float* __restrict__ rscale, float* __restrict__ part,
@@ -159,15 +159,28 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // else B). Steps past the slice are all out of range (zeros, no traffic): they keep the number
   // of DMA operations per step constant, which the vmcnt waits rely on.
   auto rsrc_a = [&](int k0) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A) + static_cast<size_t>(m0) * K + k0, 0,
-                                             0x7fffffff, kRawBufferDword3);
+    if constexpr (PACKED_A) {
+      static_assert(Cfg::BM == 256 && Cfg::BK == 32 && !SPLITK, "packed A is the 256x256x32 stage image");
+      return __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<_Float16*>(A) + static_cast<size_t>(tm) * ceil_div(K, BK) * (Cfg::A_BYTES / 2), 0, 0x7fffffff,
+          kRawBufferDword3);
+    } else {
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A) + static_cast<size_t>(m0) * K + k0, 0,
+                                               0x7fffffff, kRawBufferDword3);
+    }
   };
   auto rsrc_b = [&](int k0) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B) + static_cast<size_t>(k0) * N + n0, 0,
                                              0x7fffffff, kRawBufferDword3);
   };
   auto dma_op = [&](int st, int k0, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int d) {
-    if (d < Cfg::A_INSTR) {
+    if (d < Cfg::A_INSTR && PACKED_A) {
+      // Tile-packed A (g16_rowscale_pack_*): the stage image of step k0 is one contiguous 16 KB
+      // block; instruction q of the stage copies its q-th KB. ra is based at this tile row.
+      const int q = wave * Cfg::A_INSTR + d;
+      const uint32_t off = k0 < kend ? static_cast<uint32_t>(((k0 / BK) * 1024 + q * 64 + lane) * 16) : kOob;
+      dma16(ra, &sA[st][q * 1024], off);
+    } else if (d < Cfg::A_INSTR) {
       const int row = a_row0 + d * Cfg::A_ROWS_PER_INSTR;
       const int c = a_phys ^ swz_a<Cfg::A_ROW_CHUNKS>(row);
       const bool ok = (m0 + row < M) && (k0 + c * 8 < kend);
@@ -469,7 +482,8 @@ using GemmFn = void (*)(const _Float16*, const _Float16*, void*, const float*, c
                         int, int, int, int, int, int);
 
 template <bool OUT_F16>
-GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk) {
+GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed) {
+  if (packed) return hgemm_kernel<Cfg256, OUT_F16, false, true>;
   if (splitk) {
     switch (t) {
       case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, true>;
@@ -498,14 +512,17 @@ size_t splitk_counter_bytes(const Plan& p, int ksplit) {
 
 int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, const float* bias, const float* rscale,
                 int M, int N, int K, int ksplit, void* ws, size_t ws_bytes, uint32_t* counters_in,
-                size_t counter_bytes_in, void* stream) {
+                size_t counter_bytes_in, void* stream, bool packed = false) {
   if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0) return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
   if (ksplit < 1 || ksplit > 256) return G16_E_SPLIT;
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return G16_E_NULL;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return G16_E_ALIGN;
   const KSplit ks = ksplit_for(K, ksplit);
-  const Plan p = choose_tile(M, N, ks.ksplit > 1);
+  Plan p = choose_tile(M, N, ks.ksplit > 1);
+  if (packed) {  // the packed layout is the 256x256 tile's stage image: always that tile, no split
+    p = Plan{Tile::T256, 256, 256, ceil_div(M, 256), ceil_div(N, 256)};
+  }
   float* part = nullptr;
   uint32_t* counters = nullptr;
   if (ks.ksplit > 1) {
@@ -522,10 +539,10 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool sk = ks.ksplit > 1;
   if (out_f16)
-    return launch(gemm_fn<true>(p.tile, sk), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K, ks.kchunk,
-                  ks.ksplit, p.ntm, p.ntn);
-  return launch(gemm_fn<false>(p.tile, sk), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K, ks.kchunk,
-                ks.ksplit, p.ntm, p.ntn);
+    return launch(gemm_fn<true>(p.tile, sk, packed), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K,
+                  ks.kchunk, ks.ksplit, p.ntm, p.ntn);
+  return launch(gemm_fn<false>(p.tile, sk, packed), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K,
+                ks.kchunk, ks.ksplit, p.ntm, p.ntn);
 }
 
 }  // namespace
@@ -569,6 +586,22 @@ extern "C" int g16_hgemm_f32out(const uint16_t* A, const uint16_t* B, float* C, 
 extern "C" int g16_hgemm_f16out(const uint16_t* A, const uint16_t* B, uint16_t* C, const float* bias,
                                 const float* rscale, int M, int N, int K, void* stream) {
   return g16::gemm_launch(A, B, C, true, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream);
+}
+
+extern "C" int g16_hgemm_use_packed(int M, int N, int K, int num_cus) {
+  // The packed route pays off where the plain plan already picks the 256x256 tile without a split.
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return g16::choose_tile(M, N, false).tile == g16::Tile::T256 && g16_hgemm_plan(M, N, K, num_cus) == 1 ? 1 : 0;
+}
+
+extern "C" int g16_hgemm_packed_f32out(const uint16_t* Ap, const uint16_t* B, float* C, const float* bias,
+                                      const float* rscale, int M, int N, int K, void* stream) {
+  return g16::gemm_launch(Ap, B, C, false, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true);
+}
+
+extern "C" int g16_hgemm_packed_f16out(const uint16_t* Ap, const uint16_t* B, uint16_t* C, const float* bias,
+                                      const float* rscale, int M, int N, int K, void* stream) {
+  return g16::gemm_launch(Ap, B, C, true, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true);
 }
 
 extern "C" int g16_hgemm_splitk(const uint16_t* A, const uint16_t* B, void* C, int c_is_f16, const float* bias,

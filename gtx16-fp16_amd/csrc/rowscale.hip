@@ -13,12 +13,34 @@
 // CH 16-byte chunks of its row in registers, so the row is read from HBM once: max-reduce across
 // the wavefront (no LDS, no barrier), then scale, convert and store from the registers. Rows longer
 // than 64*CH chunks stream the remainder twice (the second read hits L2).
+//
+// Output layouts: row-major y[M,K], or the tile-packed layout the 256x256 GEMM streams (see
+// packed_a_offset): every 256-row x 32-column block of y is one contiguous 16 KB run, already in
+// the order (and LDS swizzle) the GEMM's DMA writes into LDS, so that DMA reads whole 1 KB runs
+// instead of 64-byte pieces of 256 different rows.
 #include "g16_common.hpp"
 
 namespace g16 {
 namespace {
 
 constexpr int kRowsPerBlock = 4;
+
+// Tile-packed A: blocks of kPackRows rows x kPackK columns, block (tm, ks) at block index
+// tm * ceil(K / kPackK) + ks, 16 KB each. Inside a block, 16-byte chunk q*64 + i (q = 0..15,
+// i = 0..63) holds the 8 columns 8*((i % 4) ^ ((r / 4) % 4)) .. +7 of local row r = 16q + i/4. Rows
+// past M and columns past K are zero. (This is the 256x256 GEMM's LDS stage image of A.)
+constexpr int kPackRows = 256, kPackK = 32;
+__host__ __device__ inline int packed_ksteps(int K) { return (K + kPackK - 1) / kPackK; }
+__host__ __device__ inline size_t packed_a_bytes_for(int M, int K) {
+  return static_cast<size_t>((M + kPackRows - 1) / kPackRows) * packed_ksteps(K) * (kPackRows * kPackK * 2);
+}
+// Byte offset of 16-byte chunk `oc` (columns 8*oc .. 8*oc+7) of row `row`.
+__device__ inline size_t packed_a_offset(int row, int oc, int nks) {
+  const int tm = row / kPackRows, local = row % kPackRows;
+  const int q = local / 16, ks = oc / 4, cc = oc % 4;
+  const int i = (local % 16) * 4 + (cc ^ ((local / 4) % 4));
+  return ((static_cast<size_t>(tm) * nks + ks) * 1024 + q * 64 + i) * 16;
+}
 
 __device__ inline float chunk_absmax(float m, u32x4 v, float) {
   m = fmaxf(m, fabsf(__uint_as_float(v.x)));
@@ -75,16 +97,44 @@ __device__ inline void store_scaled(_Float16* y, u32x4 v, int e, _Float16) {
   *reinterpret_cast<u32x4*>(y) = o;
 }
 
-template <typename TX, int CH>
+// Where input chunk idx of `row` goes: row-major, or tile-packed (an fp32 input chunk is half of
+// a 16-byte fp16 output chunk).
+template <typename TX, bool PACK>
+__device__ inline _Float16* out_at(_Float16* Y, int row, int K, int idx, int nks) {
+  constexpr int EPC = 16 / static_cast<int>(sizeof(TX));
+  if constexpr (!PACK) {
+    return Y + static_cast<size_t>(row) * K + static_cast<size_t>(idx) * EPC;
+  } else if constexpr (EPC == 8) {
+    return reinterpret_cast<_Float16*>(reinterpret_cast<unsigned char*>(Y) + packed_a_offset(row, idx, nks));
+  } else {
+    return reinterpret_cast<_Float16*>(reinterpret_cast<unsigned char*>(Y) + packed_a_offset(row, idx >> 1, nks) +
+                                       (idx & 1) * 8);
+  }
+}
+
+template <typename TX, int CH, bool PACK>
 __global__ __launch_bounds__(256) void rowscale_kernel(const TX* __restrict__ X, _Float16* __restrict__ Y,
                                                        float* __restrict__ S, int M, int K, int texp) {
   constexpr int EPC = 16 / static_cast<int>(sizeof(TX));  // elements per 16-byte chunk
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int nks = packed_ksteps(K);
+  if constexpr (PACK) {
+    // Padding rows of the last 256-row block are zero; real rows zero their K tail below.
+    if (row >= M) {
+      if (row < (M + kPackRows - 1) / kPackRows * kPackRows)
+        for (int oc = lane; oc < nks * 4; oc += kWave)
+          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(Y) + packed_a_offset(row, oc, nks)) =
+              u32x4{0u, 0u, 0u, 0u};
+      return;
+    }
+    for (int oc = K / 8 + lane; oc < nks * 4; oc += kWave)
+      *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(Y) + packed_a_offset(row, oc, nks)) =
+          u32x4{0u, 0u, 0u, 0u};
+  }
   if (row >= M) return;  // wave-uniform; no barriers below
   const int nch = K / EPC;
   const u32x4* xr = reinterpret_cast<const u32x4*>(X + static_cast<size_t>(row) * K);
-  _Float16* yr = Y + static_cast<size_t>(row) * K;
 
   u32x4 buf[CH];
   float amax = 0.f;
@@ -118,9 +168,10 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const TX* __restrict__ X,
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int idx = lane + c * kWave;
-    if (idx < nch) store_scaled(yr + idx * EPC, buf[c], e, TX{});
+    if (idx < nch) store_scaled(out_at<TX, PACK>(Y, row, K, idx, nks), buf[c], e, TX{});
   }
-  for (int idx = lane + CH * kWave; idx < nch; idx += kWave) store_scaled(yr + idx * EPC, xr[idx], e, TX{});
+  for (int idx = lane + CH * kWave; idx < nch; idx += kWave)
+    store_scaled(out_at<TX, PACK>(Y, row, K, idx, nks), xr[idx], e, TX{});
   if (lane == 0) S[row] = sc;
 }
 
@@ -133,7 +184,7 @@ int thresh_exponent(float thresh) {
   return static_cast<int>(ex) - 127;
 }
 
-template <typename TX, int CH>
+template <typename TX, int CH, bool PACK>
 int rowscale_launch(const void* X, void* Y, float* S, int M, int K, float thresh, void* stream) {
   if (M < 0 || K < 0 || K % 8 != 0) return G16_E_SHAPE;
   if (M == 0) return G16_OK;
@@ -141,8 +192,9 @@ int rowscale_launch(const void* X, void* Y, float* S, int M, int K, float thresh
   if (!aligned16(X) || !aligned16(Y)) return G16_E_ALIGN;
   const int texp = thresh_exponent(thresh);
   if (texp == -1000) return G16_E_SHAPE;
-  const dim3 grid(ceil_div(M, kRowsPerBlock)), block(256);
-  return launch(rowscale_kernel<TX, CH>, grid, block, static_cast<hipStream_t>(stream),
+  const int rows = PACK ? ceil_div(M, kPackRows) * kPackRows : M;
+  const dim3 grid(ceil_div(rows, kRowsPerBlock)), block(256);
+  return launch(rowscale_kernel<TX, CH, PACK>, grid, block, static_cast<hipStream_t>(stream),
                 static_cast<const TX*>(X), static_cast<_Float16*>(Y), S, M, K, texp);
 }
 
@@ -151,10 +203,25 @@ int rowscale_launch(const void* X, void* Y, float* S, int M, int K, float thresh
 
 extern "C" int g16_rowscale_f32(const float* X, uint16_t* Y, float* S, int M, int K, float thresh, void* stream) {
   // 16 chunks of 4 floats per lane: rows up to K = 4096 are read once.
-  return g16::rowscale_launch<float, 16>(X, Y, S, M, K, thresh, stream);
+  return g16::rowscale_launch<float, 16, false>(X, Y, S, M, K, thresh, stream);
 }
 
 extern "C" int g16_rowscale_f16(const uint16_t* X, uint16_t* Y, float* S, int M, int K, float thresh, void* stream) {
   // 8 chunks of 8 halves per lane: rows up to K = 4096 are read once.
-  return g16::rowscale_launch<_Float16, 8>(X, Y, S, M, K, thresh, stream);
+  return g16::rowscale_launch<_Float16, 8, false>(X, Y, S, M, K, thresh, stream);
+}
+
+extern "C" size_t g16_packed_a_bytes(int M, int K) {
+  if (M <= 0 || K <= 0) return 0;
+  return g16::packed_a_bytes_for(M, K);
+}
+
+extern "C" int g16_rowscale_pack_f32(const float* X, uint16_t* Yp, float* S, int M, int K, float thresh,
+                                     void* stream) {
+  return g16::rowscale_launch<float, 16, true>(X, Yp, S, M, K, thresh, stream);
+}
+
+extern "C" int g16_rowscale_pack_f16(const uint16_t* X, uint16_t* Yp, float* S, int M, int K, float thresh,
+                                     void* stream) {
+  return g16::rowscale_launch<_Float16, 8, true>(X, Yp, S, M, K, thresh, stream);
 }

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before libg16.so)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libg16.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -29,6 +29,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_rowscale_f16": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "g16_hgemm_f32out": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "g16_hgemm_f16out": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "g16_packed_a_bytes": (_SZ, [_I, _I]),
+    "g16_rowscale_pack_f32": (_I, [_P, _P, _P, _I, _I, _F, _P]),
+    "g16_rowscale_pack_f16": (_I, [_P, _P, _P, _I, _I, _F, _P]),
+    "g16_hgemm_packed_f32out": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "g16_hgemm_packed_f16out": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "g16_hgemm_use_packed": (_I, [_I, _I, _I, _I]),
     "g16_hgemm_splitk": (_I, [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _SZ, _P, _SZ, _P]),
     "g16_hgemm_splitk_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "g16_hgemm_splitk_counter_bytes": (_SZ, [_I, _I, _I, _I]),

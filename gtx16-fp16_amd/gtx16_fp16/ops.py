@@ -114,13 +114,26 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
         return out if out_dtype == torch.float32 else out.to(out_dtype)
 
     # GEMM path: fp16 inputs, with per-row power-of-two scaling for rows that would overflow.
-    x16 = torch.empty(M, K, device=dev, dtype=torch.float16)
     rscale = torch.empty(M, device=dev, dtype=torch.float32)
-    rs_fn = lib.g16_rowscale_f32 if x2d.dtype == torch.float32 else lib.g16_rowscale_f16
+    out = torch.empty(M, N, device=dev, dtype=out_dtype)
+    f32in = x2d.dtype == torch.float32
+    if lib.g16_hgemm_use_packed(M, N, K, cus):
+        # Large GEMM: the cast writes the fp16 copy straight into the tile-packed layout the
+        # 256x256 kernel streams (same values, same result).
+        xp = torch.empty(lib.g16_packed_a_bytes(M, K) // 2, device=dev, dtype=torch.float16)
+        rs_fn = lib.g16_rowscale_pack_f32 if f32in else lib.g16_rowscale_pack_f16
+        _clib.check(rs_fn(x2d.data_ptr(), xp.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
+                    "rowscale cast")
+        fn = lib.g16_hgemm_packed_f32out if out_dtype == torch.float32 else lib.g16_hgemm_packed_f16out
+        _clib.check(fn(xp.data_ptr(), w_t.data_ptr(), out.data_ptr(), bptr, rscale.data_ptr(), M, N, K, stream),
+                    "GEMM")
+        return out
+
+    x16 = torch.empty(M, K, device=dev, dtype=torch.float16)
+    rs_fn = lib.g16_rowscale_f32 if f32in else lib.g16_rowscale_f16
     _clib.check(rs_fn(x2d.data_ptr(), x16.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
                 "rowscale cast")
 
-    out = torch.empty(M, N, device=dev, dtype=out_dtype)
     ksplit = lib.g16_hgemm_plan(M, N, K, cus)
     if ksplit > 1:
         # Too few output tiles to fill the GPU: split K, reduce the slices in a fixed order.
