@@ -59,6 +59,8 @@ def parse(argv=None):
                          "calibration for FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--bert", action="store_true",
                     help="time only the BERT-base configuration (fp32 vs patch()) and print its JSON line")
+    ap.add_argument("--overhead", action="store_true",
+                    help="time only the per-call cost of FastLinear vs nn.Linear at one token and print it")
     return ap.parse_args(argv)
 
 
@@ -273,6 +275,39 @@ def bench_all(torch, g, steps: int, dev) -> list:
     del x, w
     rows.append(bench_bert(torch, g, dev))
     print(json.dumps(rows[-1]), flush=True)
+    rows.extend(bench_overhead(torch, g, dev))
+    return rows
+
+
+def bench_overhead(torch, g, dev, n: int = 1000) -> list:
+    """Per-call host cost and wall time of FastLinear vs nn.Linear at one token (the decode path),
+    as bench/overhead.py:9-29 of the reference measures it: `cpu` is the time to enqueue n calls,
+    `wall` the time until they have also finished on the GPU."""
+    import torch.nn as nn
+
+    def cost(fn):
+        with torch.no_grad():
+            for _ in range(50):
+                fn()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            for _ in range(n):
+                fn()
+            cpu = (time.perf_counter() - t) / n
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t) / n
+        return round(cpu * 1e6, 2), round(wall * 1e6, 2)
+
+    rows = []
+    for K, N in ((1024, 1024), (1024, 3072), (3072, 1024), (4096, 4096)):
+        torch.manual_seed(0)
+        lin = nn.Linear(K, N).to(dev)
+        fl = g.FastLinear.from_linear(lin)
+        x = torch.randn(1, 1, K, device=dev)
+        a, b = cost(lambda: lin(x)), cost(lambda: fl(x))
+        rows.append({"config": f"decode overhead 1x{K}x{N}", "nn_linear_cpu_us": a[0], "nn_linear_wall_us": a[1],
+                     "fast_linear_cpu_us": b[0], "fast_linear_wall_us": b[1]})
+        print(json.dumps(rows[-1]), flush=True)
     return rows
 
 
@@ -427,6 +462,9 @@ def main(argv=None) -> int:
         return 0
     if args.bert:
         print(json.dumps(bench_bert(torch, g, dev)), flush=True)
+        return 0
+    if args.overhead:
+        bench_overhead(torch, g, dev)
         return 0
     configs = bench_all(torch, g, args.steps, dev) if args.all else None
     c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev)
