@@ -99,6 +99,26 @@ __device__ inline void reset_counter(uint32_t* counter) {
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Tile-packed operand layout of the 256x256 GEMM (activations from the rowscale cast, weights from
+// g16_pack_weight). An operand with R rows (rows = M for activations, N for the transposed
+// weight) and K columns is stored as blocks of kPackRows rows x kPackK columns; block (t, ks) is at
+// block index t * ceil(K / kPackK) + ks, 16 KB each. Inside a block, 16-byte chunk q*64 + i
+// (q < 16, i < 64) holds columns 8*((i % 4) ^ ((r / 4) % 4)) .. +7 of local row r = 16q + i/4.
+// Rows >= R and columns >= K are zero. This is the GEMM's LDS stage image, so its DMA copies whole
+// 1 KB runs.
+constexpr int kPackRows = 256, kPackK = 32;
+__host__ __device__ inline int packed_ksteps(int K) { return (K + kPackK - 1) / kPackK; }
+__host__ __device__ inline size_t packed_bytes_for(int R, int K) {
+  return static_cast<size_t>((R + kPackRows - 1) / kPackRows) * packed_ksteps(K) * (kPackRows * kPackK * 2);
+}
+// Byte offset of 16-byte chunk `oc` (columns 8*oc .. 8*oc+7) of row `row`.
+__device__ inline size_t packed_offset(int row, int oc, int nks) {
+  const int t = row / kPackRows, local = row % kPackRows;
+  const int q = local / 16, ks = oc / 4, cc = oc % 4;
+  const int i = (local % 16) * 4 + (cc ^ ((local / 4) % 4));
+  return ((static_cast<size_t>(t) * nks + ks) * 1024 + q * 64 + i) * 16;
+}
+
 __device__ inline float h2f(_Float16 h) { return static_cast<float>(h); }
 __device__ inline float to_f(float x) { return x; }
 __device__ inline float to_f(_Float16 x) { return static_cast<float>(x); }

@@ -117,7 +117,7 @@ __device__ inline void wait_dma_le() {
 // compiler from moving LDS accesses across it.
 __device__ inline void phase_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <class Cfg, bool OUT_F16, bool SPLITK, bool PACKED_A = false>
+template <class Cfg, bool OUT_F16, bool SPLITK, bool PACKED_A = false, bool PACKED_B = false>
 __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
                                                          void* __restrict__ Cv, const float* __restrict__ bias,
                                                          const float* __restrict__ rscale, float* __restrict__ part,
@@ -170,8 +170,15 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     }
   };
   auto rsrc_b = [&](int k0) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B) + static_cast<size_t>(k0) * N + n0, 0,
-                                             0x7fffffff, kRawBufferDword3);
+    if constexpr (PACKED_B) {
+      static_assert(PACKED_A && Cfg::BN == 256, "a packed weight pairs with packed activations on the 256 tile");
+      return __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<_Float16*>(B) + static_cast<size_t>(tn) * ceil_div(K, BK) * (Cfg::B_BYTES / 2), 0, 0x7fffffff,
+          kRawBufferDword3);
+    } else {
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B) + static_cast<size_t>(k0) * N + n0, 0,
+                                               0x7fffffff, kRawBufferDword3);
+    }
   };
   auto dma_op = [&](int st, int k0, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int d) {
     if (d < Cfg::A_INSTR && PACKED_A) {
@@ -186,6 +193,11 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       const bool ok = (m0 + row < M) && (k0 + c * 8 < kend);
       const uint32_t off = ok ? static_cast<uint32_t>((row * K + c * 8) * 2) : kOob;
       dma16(ra, &sA[st][(wave * Cfg::A_INSTR + d) * 1024], off);
+    } else if (PACKED_B) {
+      // Packed weight (g16_pack_weight): B^T's stage image, like packed A.
+      const int q = wave * Cfg::B_INSTR + (d - Cfg::A_INSTR);
+      const uint32_t off = k0 < kend ? static_cast<uint32_t>(((k0 / BK) * 1024 + q * 64 + lane) * 16) : kOob;
+      dma16(rb, &sB[st][q * 1024], off);
     } else {
       const int i = d - Cfg::A_INSTR;
       const int row = b_row0 + i * Cfg::B_ROWS_PER_INSTR;
@@ -235,6 +247,13 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     const int ks = f / (TM + TN), w = f % (TM + TN);
     if (w < TM) {
       af[buf][ks][w] = *reinterpret_cast<const half8*>(&sA[st][a_off(w, ks)]);
+    } else if constexpr (PACKED_B) {
+      // B^T stored [n][k] like A: one 16-byte read gives lane l the k-run of column l%32.
+      const int j = w - TM;
+      const int row = wn0 + 32 * j + frow;
+      const int chunk = ks * 2 + fk;
+      bf[buf][ks][j] = *reinterpret_cast<const half8*>(
+          &sB[st][row * (BK * 2) + ((chunk ^ swz_a<Cfg::A_ROW_CHUNKS>(row)) * 16)]);
     } else {
       const int j = w - TM;
       const int krow = ks * 16 + b_k_in;
@@ -482,7 +501,8 @@ using GemmFn = void (*)(const _Float16*, const _Float16*, void*, const float*, c
                         int, int, int, int, int, int);
 
 template <bool OUT_F16>
-GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed) {
+GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b) {
+  if (packed_b) return hgemm_kernel<Cfg256, OUT_F16, false, true, true>;
   if (packed) return hgemm_kernel<Cfg256, OUT_F16, false, true>;
   if (splitk) {
     switch (t) {
@@ -512,7 +532,7 @@ size_t splitk_counter_bytes(const Plan& p, int ksplit) {
 
 int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, const float* bias, const float* rscale,
                 int M, int N, int K, int ksplit, void* ws, size_t ws_bytes, uint32_t* counters_in,
-                size_t counter_bytes_in, void* stream, bool packed = false) {
+                size_t counter_bytes_in, void* stream, bool packed = false, bool packed_b = false) {
   if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0) return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
   if (ksplit < 1 || ksplit > 256) return G16_E_SPLIT;
@@ -539,9 +559,9 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool sk = ks.ksplit > 1;
   if (out_f16)
-    return launch(gemm_fn<true>(p.tile, sk, packed), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K,
+    return launch(gemm_fn<true>(p.tile, sk, packed, packed_b), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K,
                   ks.kchunk, ks.ksplit, p.ntm, p.ntn);
-  return launch(gemm_fn<false>(p.tile, sk, packed), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K,
+  return launch(gemm_fn<false>(p.tile, sk, packed, packed_b), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K,
                 ks.kchunk, ks.ksplit, p.ntm, p.ntn);
 }
 
@@ -602,6 +622,16 @@ extern "C" int g16_hgemm_packed_f32out(const uint16_t* Ap, const uint16_t* B, fl
 extern "C" int g16_hgemm_packed_f16out(const uint16_t* Ap, const uint16_t* B, uint16_t* C, const float* bias,
                                       const float* rscale, int M, int N, int K, void* stream) {
   return g16::gemm_launch(Ap, B, C, true, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true);
+}
+
+extern "C" int g16_hgemm_packed_ab_f32out(const uint16_t* Ap, const uint16_t* Bp, float* C, const float* bias,
+                                         const float* rscale, int M, int N, int K, void* stream) {
+  return g16::gemm_launch(Ap, Bp, C, false, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true, true);
+}
+
+extern "C" int g16_hgemm_packed_ab_f16out(const uint16_t* Ap, const uint16_t* Bp, uint16_t* C, const float* bias,
+                                         const float* rscale, int M, int N, int K, void* stream) {
+  return g16::gemm_launch(Ap, Bp, C, true, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true, true);
 }
 
 extern "C" int g16_hgemm_splitk(const uint16_t* A, const uint16_t* B, void* C, int c_is_f16, const float* bias,

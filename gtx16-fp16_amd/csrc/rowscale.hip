@@ -15,32 +15,15 @@
 // than 64*CH chunks stream the remainder twice (the second read hits L2).
 //
 // Output layouts: row-major y[M,K], or the tile-packed layout the 256x256 GEMM streams (see
-// packed_a_offset): every 256-row x 32-column block of y is one contiguous 16 KB run, already in
-// the order (and LDS swizzle) the GEMM's DMA writes into LDS, so that DMA reads whole 1 KB runs
-// instead of 64-byte pieces of 256 different rows.
+// packed_offset in g16_common.hpp): every 256-row x 32-column block of y is one contiguous 16 KB
+// run, already in the order (and LDS swizzle) the GEMM's DMA writes into LDS, so that DMA reads
+// whole 1 KB runs instead of 64-byte pieces of 256 different rows.
 #include "g16_common.hpp"
 
 namespace g16 {
 namespace {
 
 constexpr int kRowsPerBlock = 4;
-
-// Tile-packed A: blocks of kPackRows rows x kPackK columns, block (tm, ks) at block index
-// tm * ceil(K / kPackK) + ks, 16 KB each. Inside a block, 16-byte chunk q*64 + i (q = 0..15,
-// i = 0..63) holds the 8 columns 8*((i % 4) ^ ((r / 4) % 4)) .. +7 of local row r = 16q + i/4. Rows
-// past M and columns past K are zero. (This is the 256x256 GEMM's LDS stage image of A.)
-constexpr int kPackRows = 256, kPackK = 32;
-__host__ __device__ inline int packed_ksteps(int K) { return (K + kPackK - 1) / kPackK; }
-__host__ __device__ inline size_t packed_a_bytes_for(int M, int K) {
-  return static_cast<size_t>((M + kPackRows - 1) / kPackRows) * packed_ksteps(K) * (kPackRows * kPackK * 2);
-}
-// Byte offset of 16-byte chunk `oc` (columns 8*oc .. 8*oc+7) of row `row`.
-__device__ inline size_t packed_a_offset(int row, int oc, int nks) {
-  const int tm = row / kPackRows, local = row % kPackRows;
-  const int q = local / 16, ks = oc / 4, cc = oc % 4;
-  const int i = (local % 16) * 4 + (cc ^ ((local / 4) % 4));
-  return ((static_cast<size_t>(tm) * nks + ks) * 1024 + q * 64 + i) * 16;
-}
 
 __device__ inline float chunk_absmax(float m, u32x4 v, float) {
   m = fmaxf(m, fabsf(__uint_as_float(v.x)));
@@ -105,9 +88,9 @@ __device__ inline _Float16* out_at(_Float16* Y, int row, int K, int idx, int nks
   if constexpr (!PACK) {
     return Y + static_cast<size_t>(row) * K + static_cast<size_t>(idx) * EPC;
   } else if constexpr (EPC == 8) {
-    return reinterpret_cast<_Float16*>(reinterpret_cast<unsigned char*>(Y) + packed_a_offset(row, idx, nks));
+    return reinterpret_cast<_Float16*>(reinterpret_cast<unsigned char*>(Y) + packed_offset(row, idx, nks));
   } else {
-    return reinterpret_cast<_Float16*>(reinterpret_cast<unsigned char*>(Y) + packed_a_offset(row, idx >> 1, nks) +
+    return reinterpret_cast<_Float16*>(reinterpret_cast<unsigned char*>(Y) + packed_offset(row, idx >> 1, nks) +
                                        (idx & 1) * 8);
   }
 }
@@ -124,12 +107,12 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const TX* __restrict__ X,
     if (row >= M) {
       if (row < (M + kPackRows - 1) / kPackRows * kPackRows)
         for (int oc = lane; oc < nks * 4; oc += kWave)
-          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(Y) + packed_a_offset(row, oc, nks)) =
+          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(Y) + packed_offset(row, oc, nks)) =
               u32x4{0u, 0u, 0u, 0u};
       return;
     }
     for (int oc = K / 8 + lane; oc < nks * 4; oc += kWave)
-      *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(Y) + packed_a_offset(row, oc, nks)) =
+      *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(Y) + packed_offset(row, oc, nks)) =
           u32x4{0u, 0u, 0u, 0u};
   }
   if (row >= M) return;  // wave-uniform; no barriers below
@@ -213,7 +196,7 @@ extern "C" int g16_rowscale_f16(const uint16_t* X, uint16_t* Y, float* S, int M,
 
 extern "C" size_t g16_packed_a_bytes(int M, int K) {
   if (M <= 0 || K <= 0) return 0;
-  return g16::packed_a_bytes_for(M, K);
+  return g16::packed_bytes_for(M, K);
 }
 
 extern "C" int g16_rowscale_pack_f32(const float* X, uint16_t* Yp, float* S, int M, int K, float thresh,

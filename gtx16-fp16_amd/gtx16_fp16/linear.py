@@ -10,7 +10,7 @@ import torch.nn.functional as F
 
 from . import _clib
 from .kernels import SKINNY_MAX_M, PreparedLaunch, split_buffers, stream_handle
-from .ops import _is_target, _sm_count, is_affected, mm_t, supported
+from .ops import _is_target, _sm_count, is_affected, mm_t, mm_t_prepacked, pack_weight, prepacked_route, supported
 
 
 class FastLinear(nn.Module):
@@ -23,7 +23,13 @@ class FastLinear(nn.Module):
       of two, then scaled back in fp32), multiply on the matrix cores, accumulate in fp32.
     - Output dtype follows the input dtype (fp32 in -> fp32 out; other dtypes -> fp32).
     - When autograd is needed or the shape is unsupported, falls back to F.linear.
+    - For large batches on the 256x256 GEMM route the layer also keeps a prepacked copy of its
+      weight (built on first use, rebuilt when ``weight_t`` changes or moves; not part of the
+      state_dict), which the GEMM reads with plain 16-byte loads. It costs one more copy of the
+      fp16 weight; set ``prepack_weight = False`` (class or instance) to do without it.
     """
+
+    prepack_weight = True
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True, device=None):
         super().__init__()
@@ -31,6 +37,9 @@ class FastLinear(nn.Module):
         # (M, device index) -> (PreparedLaunch, ksplit, (partial, counter) bytes, weight pointer), or None when
         # the weight is not supported by the kernels (token-by-token fast path).
         self._skinny: dict = {}
+        # prepacked weight for the large-GEMM route and the (pointer, version) of weight_t it was built from
+        self._wp: torch.Tensor | None = None
+        self._wp_key: tuple | None = None
         self.register_buffer("weight_t", torch.empty(in_features, out_features, dtype=torch.float16, device=device))
         self.register_buffer("bias", torch.empty(out_features, dtype=torch.float32, device=device) if bias else None)
 
@@ -67,6 +76,14 @@ class FastLinear(nn.Module):
             self._skinny[key] = entry
         return entry
 
+    def _packed_weight(self) -> torch.Tensor:
+        w = self.weight_t
+        key = (w.data_ptr(), w._version, w.device)
+        if self._wp is None or self._wp_key != key:
+            self._wp = pack_weight(w)
+            self._wp_key = key
+        return self._wp
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         out_dtype = x.dtype if x.dtype in (torch.float32, torch.float16) else torch.float32
         if torch.is_grad_enabled() and x.requires_grad:
@@ -96,7 +113,13 @@ class FastLinear(nn.Module):
         if x2.shape[0] == 0 or not supported(x2, self.weight_t):
             y = F.linear(x2.float(), self.weight_t.t().float(), self.bias)
         else:
-            y = mm_t(x2, self.weight_t, self.bias, torch.float32 if out_dtype == torch.float32 else torch.float16)
+            odt = torch.float32 if out_dtype == torch.float32 else torch.float16
+            M = x2.shape[0]
+            if self.prepack_weight and M > SKINNY_MAX_M and \
+                    prepacked_route(M, self.out_features, self.in_features, x2.device):
+                y = mm_t_prepacked(x2, self.weight_t, self._packed_weight(), self.bias, odt)
+            else:
+                y = mm_t(x2, self.weight_t, self.bias, odt)
         return y.reshape(*shape[:-1], self.out_features).to(out_dtype)
 
     def extra_repr(self) -> str:

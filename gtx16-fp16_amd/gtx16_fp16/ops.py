@@ -150,6 +150,54 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
     return out
 
 
+def prepacked_route(M: int, N: int, K: int, device: torch.device) -> bool:
+    """True where mm_t takes the tile-packed 256x256 route, the one a prepacked weight serves."""
+    return bool(_clib.load().g16_hgemm_use_packed(M, N, K, _sm_count(device)))
+
+
+def pack_weight(w_t: torch.Tensor) -> torch.Tensor:
+    """w_t [K, N] fp16 (CUDA, contiguous, K and N multiples of 8) -> its prepacked form for
+    mm_t_prepacked: w_t transposed into the GEMM's tile-packed layout, a 1-D fp16 tensor."""
+    lib = _clib.load()
+    K, N = w_t.shape
+    wp = torch.empty(lib.g16_packed_b_bytes(K, N) // 2, device=w_t.device, dtype=torch.float16)
+    _clib.check(lib.g16_pack_weight(w_t.data_ptr(), wp.data_ptr(), K, N, stream_handle(w_t.device.index or 0)),
+                "weight packing")
+    return wp
+
+
+def mm_t_prepacked(x2d: torch.Tensor, w_t: torch.Tensor, wp: torch.Tensor, bias: torch.Tensor | None = None,
+                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """mm_t for a weight that also has its prepacked form ``wp = pack_weight(w_t)``: same contract and
+    the same result bits as ``mm_t(x2d, w_t, bias, out_dtype)``. On the large-GEMM route the GEMM
+    reads ``wp`` instead of ``w_t`` (plain 16-byte LDS reads for both operands); elsewhere it is
+    exactly mm_t. Check supported(x2d, w_t) first."""
+    if out_dtype not in (torch.float32, torch.float16):
+        raise ValueError(f"out_dtype must be float32 or float16, got {out_dtype}")
+    M, K = x2d.shape
+    N = w_t.shape[1]
+    dev = x2d.device
+    if M <= SKINNY_MAX_M or not prepacked_route(M, N, K, dev):
+        return mm_t(x2d, w_t, bias, out_dtype)
+    lib = _clib.load()
+    if wp.dtype != torch.float16 or wp.device != dev or not wp.is_contiguous() or \
+            wp.numel() * 2 < lib.g16_packed_b_bytes(K, N) or wp.data_ptr() % 16 != 0:
+        raise ValueError("wp is not a packed weight for this w_t (use pack_weight(w_t))")
+    stream = stream_handle(dev.index or 0)
+    b = None if bias is None else bias.float().contiguous()
+    x2d = _aligned(x2d)
+    rscale = torch.empty(M, device=dev, dtype=torch.float32)
+    out = torch.empty(M, N, device=dev, dtype=out_dtype)
+    xp = torch.empty(lib.g16_packed_a_bytes(M, K) // 2, device=dev, dtype=torch.float16)
+    rs_fn = lib.g16_rowscale_pack_f32 if x2d.dtype == torch.float32 else lib.g16_rowscale_pack_f16
+    _clib.check(rs_fn(x2d.data_ptr(), xp.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
+                "rowscale cast")
+    fn = lib.g16_hgemm_packed_ab_f32out if out_dtype == torch.float32 else lib.g16_hgemm_packed_ab_f16out
+    _clib.check(fn(xp.data_ptr(), wp.data_ptr(), out.data_ptr(), None if b is None else b.data_ptr(),
+                   rscale.data_ptr(), M, N, K, stream), "GEMM")
+    return out
+
+
 def matmul(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """Drop-in for a @ b with 2-D fp16 inputs; falls back to torch.matmul when the shape is not
     supported. Default output dtype: fp16, like torch (ops.py:111-119)."""

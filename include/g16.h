@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 3
+#define G16_ABI_VERSION 4
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -103,6 +103,21 @@ int g16_hgemm_packed_f32out(const uint16_t* Ap, const uint16_t* B, float* C, con
 int g16_hgemm_packed_f16out(const uint16_t* Ap, const uint16_t* B, uint16_t* C, const float* bias,
                             const float* rscale, int M, int N, int K, void* stream);
 int g16_hgemm_use_packed(int M, int N, int K, int num_cus);
+
+/* ---------------------------------------------------------------------------------------------
+ * Prepacked weight for the large GEMM (no counterpart kernel in the reference; it serves
+ * FastLinear, src/gtx16_fp16/linear.py:12-76, whose fp16 weight_t [K,N] is fixed after from_linear,
+ * linear.py:30-37). g16_pack_weight writes w_t transposed ([N,K]) in the tile-packed layout above
+ * (rows = N); g16_hgemm_packed_ab_* is the 256x256 GEMM with both operands packed. Same values and
+ * the same result bits as g16_hgemm_packed_* on the unpacked weight.
+ */
+size_t g16_packed_b_bytes(int K, int N);
+int g16_pack_weight(const uint16_t* w_t, uint16_t* wp, int K, int N, void* stream);
+int g16_hgemm_packed_ab_f32out(const uint16_t* Ap, const uint16_t* Bp, float* C, const float* bias,
+                               const float* rscale, int M, int N, int K, void* stream);
+int g16_hgemm_packed_ab_f16out(const uint16_t* Ap, const uint16_t* Bp, uint16_t* C,
+                               const float* bias, const float* rscale, int M, int N, int K,
+                               void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Deterministic split-K GEMM for shapes with too few output tiles to fill the GPU.

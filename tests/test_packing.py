@@ -47,3 +47,13 @@ def test_library_packed_sizes_and_routing():
     assert lib.g16_hgemm_use_packed(65536, 3072, 768, 256) == 1
     assert lib.g16_hgemm_use_packed(64, 1024, 4096, 256) == 0     # split-K shape
     assert lib.g16_hgemm_use_packed(300, 264, 136, 256) == 0      # small: 128x128 tiles
+
+
+def test_library_packed_weight_size():
+    from gtx16_fp16 import _clib
+
+    lib = _clib.load()
+    for K, N in [(8, 8), (136, 264), (4096, 4096), (768, 3072)]:
+        assert lib.g16_packed_b_bytes(K, N) == 2 * packed_elems(N, K)
+    assert lib.g16_packed_b_bytes(0, 8) == 0
+    assert lib.g16_pack_weight(None, None, 12, 8, None) == -1   # K % 8
