@@ -59,6 +59,8 @@ def parse(argv=None):
                          "calibration for FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--bert", action="store_true",
                     help="time only the BERT-base configuration (fp32 vs patch()) and print its JSON line")
+    ap.add_argument("--peak", action="store_true",
+                    help="measure this part's fp32/fp16 VALU, MFMA and HBM read peaks and print them")
     ap.add_argument("--overhead", action="store_true",
                     help="time only the per-call cost of FastLinear vs nn.Linear at one token and print it")
     return ap.parse_args(argv)
@@ -311,6 +313,57 @@ def bench_overhead(torch, g, dev, n: int = 1000) -> list:
     return rows
 
 
+def bench_peak(torch, lib, dev) -> list:
+    """Instruction and HBM peaks of this part (the analogue of the reference's bench/peak.py):
+    fp32 FMA, packed fp16 FMA and the two fp16 MFMA shapes from register-only loops, and a
+    streaming read of a 4 GiB buffer. Each is the best of 3 timed launches after a warm-up."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rows = []
+    for kind, name, waves_per_simd, iters in ((0, "fp32 FMA (VALU)", 8, 20000), (1, "packed fp16 FMA (VALU)", 8, 20000),
+                                              (2, "MFMA f16 32x32x16", 2, 20000), (3, "MFMA f16 16x16x32", 2, 20000)):
+        blocks = cus * waves_per_simd  # 256-lane workgroups: 4 wavefronts each, one per SIMD
+        out = torch.empty(blocks * 256, device=dev)
+        _clib_ok(lib.g16_peak_run(kind, blocks, 100, out.data_ptr(), stream))
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            _clib_ok(lib.g16_peak_run(kind, blocks, iters, out.data_ptr(), stream))
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e-3)
+        flop = lib.g16_peak_flops_per_lane_iter(kind) * blocks * 256 * iters
+        rows.append({"peak": name, "TFLOP/s": round(flop / best / 1e12, 1), "ms": round(best * 1e3, 3)})
+        print(json.dumps(rows[-1]), flush=True)
+    nbytes = 4 << 30
+    buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    for per_cu in (4, 8, 16):  # workgroups of 256 lanes per CU, 8 loads in flight per lane
+        blocks = cus * per_cu
+        out = torch.empty(blocks * 256, device=dev)
+        _clib_ok(lib.g16_stream_read(buf.data_ptr(), nbytes, blocks, out.data_ptr(), stream))
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            _clib_ok(lib.g16_stream_read(buf.data_ptr(), nbytes, blocks, out.data_ptr(), stream))
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e-3)
+        rows.append({"peak": f"HBM read stream (4 GiB, 16-byte loads, {per_cu} workgroups/CU)",
+                     "GB/s": round(nbytes / best / 1e9, 1), "ms": round(best * 1e3, 3)})
+        print(json.dumps(rows[-1]), flush=True)
+    del buf
+    return rows
+
+
+def _clib_ok(status: int) -> None:
+    if status != 0:
+        raise RuntimeError(f"peak kernel launch failed with status {status}")
+
+
 def bench_bert(torch, g, dev, reps: int = 3) -> dict:
     """C5: random-init BERT-base, 256 x 256 token ids, fp32 forward, then patch() and again; tokens/s
     of each and the cosine of the mean-pooled (and CLS) embeddings."""
@@ -465,6 +518,9 @@ def main(argv=None) -> int:
         return 0
     if args.overhead:
         bench_overhead(torch, g, dev)
+        return 0
+    if args.peak:
+        bench_peak(torch, lib, dev)
         return 0
     configs = bench_all(torch, g, args.steps, dev) if args.all else None
     c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev)

@@ -1,0 +1,144 @@
+// Instruction and bandwidth peaks of the part the kernels run on: the MI355X counterpart of the
+// reference's bench/peak.py:1-63 (FFMA / HFMA2 / mma.sync on Turing). It calibrates the
+// denominators the benchmark's rooflines use, under the clocks the part actually holds.
+//
+//   kind 0: fp32 FMA on the VALU (v_fma_f32), 8 independent chains per lane;
+//   kind 1: packed fp16 FMA (v_pk_fma_f16), 8 chains of half2 per lane;
+//   kind 2: v_mfma_f32_32x32x16_f16, 8 independent accumulators per wavefront;
+//   kind 3: v_mfma_f32_16x16x32_f16, 16 independent accumulators per wavefront;
+// and a streaming read of a large buffer (16-byte loads, grid-stride) for HBM bandwidth.
+// Everything stays in registers except the read stream; results are folded into `out` so the
+// compiler cannot drop the work.
+#include "g16_common.hpp"
+
+namespace g16 {
+namespace {
+
+typedef _Float16 half2x __attribute__((ext_vector_type(2)));
+
+__global__ __launch_bounds__(256) void peak_ffma(float* out, float a, float b, int iters) {
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(threadIdx.x + i);
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = fmaf(x[i], a, b);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += x[i];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+__global__ __launch_bounds__(256) void peak_hfma2(float* out, float af, float bf, int iters) {
+  const half2x a = {static_cast<_Float16>(af), static_cast<_Float16>(af)};
+  const half2x b = {static_cast<_Float16>(bf), static_cast<_Float16>(bf)};
+  half2x x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const _Float16 v = static_cast<_Float16>((threadIdx.x + i) * 1e-3f);
+    x[i] = half2x{v, v};
+  }
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = x[i] * a + b;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += static_cast<float>(x[i].x) + static_cast<float>(x[i].y);
+  out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+__global__ __launch_bounds__(256) void peak_mfma32(float* out, float seed, int iters) {
+  float16v acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = float16v{};
+  half8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = static_cast<_Float16>(seed * (threadIdx.x + i));
+    b[i] = static_cast<_Float16>(seed * i);
+  }
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += acc[i][threadIdx.x & 15];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+__global__ __launch_bounds__(256) void peak_mfma16(float* out, float seed, int iters) {
+  float4v acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
+  half8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = static_cast<_Float16>(seed * (threadIdx.x + i));
+    b[i] = static_cast<_Float16>(seed * i);
+  }
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i], 0, 0, 0);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += acc[i][threadIdx.x & 3];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// Grid-stride read of n16 16-byte chunks; every lane folds what it read into one float.
+__global__ __launch_bounds__(256) void stream_read(const u32x4* __restrict__ p, size_t n16, float* out) {
+  uint32_t acc = 0;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  constexpr int kDepth = 8;  // loads in flight per lane
+  for (; i + (kDepth - 1) * stride < n16; i += kDepth * stride) {
+    u32x4 v[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) v[d] = p[i + d * stride];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) acc ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+  }
+  for (; i < n16; i += stride) {
+    const u32x4 v = p[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  out[blockIdx.x * blockDim.x + threadIdx.x] = static_cast<float>(acc & 0xffu);
+}
+
+}  // namespace
+}  // namespace g16
+
+extern "C" double g16_peak_flops_per_lane_iter(int kind) {
+  // flops one lane contributes per loop iteration (MFMA: a wavefront's flops / 64)
+  switch (kind) {
+    case 0: return 8.0 * 2;                          // 8 fp32 FMAs
+    case 1: return 8.0 * 2 * 2;                      // 8 packed fp16 FMAs
+    case 2: return 8.0 * 32 * 32 * 16 * 2 / 64;      // 8 MFMA 32x32x16
+    case 3: return 16.0 * 16 * 16 * 32 * 2 / 64;     // 16 MFMA 16x16x32
+    default: return 0.0;
+  }
+}
+
+extern "C" int g16_peak_run(int kind, int blocks, int iters, float* out, void* stream) {
+  // out must hold blocks * 256 floats
+  if (blocks <= 0 || iters < 0) return G16_E_SHAPE;
+  if (out == nullptr) return G16_E_NULL;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (kind) {
+    case 0: return g16::launch(g16::peak_ffma, grid, block, s, out, 0.999f, 0.001f, iters);
+    case 1: return g16::launch(g16::peak_hfma2, grid, block, s, out, 0.999f, 0.001f, iters);
+    case 2: return g16::launch(g16::peak_mfma32, grid, block, s, out, 1e-3f, iters);
+    case 3: return g16::launch(g16::peak_mfma16, grid, block, s, out, 1e-3f, iters);
+    default: return G16_E_DTYPE;
+  }
+}
+
+extern "C" int g16_stream_read(const void* buf, size_t bytes, int blocks, float* out, void* stream) {
+  // out must hold blocks * 256 floats; bytes must be a multiple of 16
+  if (blocks <= 0 || bytes % 16 != 0) return G16_E_SHAPE;
+  if (buf == nullptr || out == nullptr) return G16_E_NULL;
+  if (!g16::aligned16(buf)) return G16_E_ALIGN;
+  return g16::launch(g16::stream_read, dim3(static_cast<unsigned>(blocks)), dim3(256), static_cast<hipStream_t>(stream),
+                     static_cast<const g16::u32x4*>(buf), bytes / 16, out);
+}

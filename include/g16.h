@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 4
+#define G16_ABI_VERSION 5
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -155,6 +155,20 @@ int g16_skinny_f16in(const uint16_t* A, const uint16_t* B, float* C, const float
 size_t g16_skinny_workspace_bytes(int M, int N, int K, int ksplit);
 size_t g16_skinny_counter_bytes(int M, int N, int K, int ksplit);
 int g16_skinny_plan(int M, int N, int K, int num_cus);
+
+/* ---------------------------------------------------------------------------------------------
+ * Peak microbenchmark: the MI355X counterpart of the reference's bench/peak.py:1-63 (which times
+ * FFMA, HFMA2 and mma.sync kernels). No counterpart in the kernel ABI: it measures the instruction
+ * and bandwidth peaks the benchmark's rooflines divide by, at the clocks the part holds.
+ * kind 0: fp32 FMA (VALU); 1: packed fp16 FMA; 2: MFMA 32x32x16 f16; 3: MFMA 16x16x32 f16.
+ * g16_peak_run launches `blocks` workgroups of 256 lanes looping `iters` times; each lane does
+ * g16_peak_flops_per_lane_iter(kind) flops per iteration. `out` holds blocks * 256 floats.
+ * g16_stream_read reads `bytes` (a multiple of 16, 16-byte aligned buffer) once with 16-byte
+ * loads from `blocks` workgroups of 256 lanes; `out` holds blocks * 256 floats.
+ */
+double g16_peak_flops_per_lane_iter(int kind);
+int g16_peak_run(int kind, int blocks, int iters, float* out, void* stream);
+int g16_stream_read(const void* buf, size_t bytes, int blocks, float* out, void* stream);
 
 #ifdef __cplusplus
 }
