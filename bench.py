@@ -387,6 +387,18 @@ def bench_bert(torch, g, dev, reps: int = 3) -> dict:
     n = g.patch(model)
     torch.cuda.empty_cache()
     out, t16 = timed()
+    # activation ranges the patched linears see (reference bench/diag_ranges.py), on 16 sequences
+    from gtx16_fp16.diag import range_hooks, risky
+
+    stats, handles = range_hooks(model)
+    embeddings(model, ids[:16])
+    for h in handles:
+        h.remove()
+    ranges = {"layers": len(stats), "layers_needing_care": len(risky(stats)),
+              "rows_rescaled": sum(v["rows_rescaled"] for v in stats.values()),
+              "rows_seen": sum(v["rows"] for v in stats.values()),
+              "max_exponent": max((v["max_exponent"] for v in stats.values()), default=0),
+              "x_amax": round(max((v["x_amax"] for v in stats.values()), default=0.0), 2)}
     cos = [F.cosine_similarity(o.double(), r.double(), dim=1) for o, r in zip(out, ref)]
     tokens = ids.numel()
     # Linear work per forward: 12 layers x (4 x 768^2 + 2 x 768 x 3072) MACs per token, plus the pooler.
@@ -399,7 +411,7 @@ def bench_bert(torch, g, dev, reps: int = 3) -> dict:
             "ms_per_forward": round(t16 * 1e3, 2), "fp32_ms_per_forward": round(t32 * 1e3, 2),
             "linear_TFLOPS_equiv": round(lin_flop / t16 / 1e12, 1),
             "cosine_mean_pooled_min": round(cos[0].min().item(), 8),
-            "cosine_cls_min": round(cos[1].min().item(), 8)}
+            "cosine_cls_min": round(cos[1].min().item(), 8), "activation_ranges": ranges}
 
 
 def cpu_baseline(torch) -> dict:
