@@ -76,6 +76,36 @@ def skinny_config(N: int, K: int, sms: int) -> tuple[tuple[int, int, int], int]:
     return ((N + 511) // 512 * ksplit, 1, 1), rows
 
 
+# (M, N, K, device index) -> the GEMM route mm_t takes for that shape, computed once per shape:
+# ("packed", packed-activation bytes) | ("splitk", ksplit, partial bytes, counter bytes) | ("plain",);
+# skinny shapes are keyed (-M, N, K, device index) -> (ksplit, partial bytes, counter bytes).
+_routes: dict[tuple[int, int, int, int], tuple] = {}
+
+
+def _gemm_route(lib, M: int, N: int, K: int, dev: torch.device) -> tuple:
+    key = (M, N, K, dev.index or 0)
+    r = _routes.get(key)
+    if r is None:
+        cus = _sm_count(dev)
+        if lib.g16_hgemm_use_packed(M, N, K, cus):
+            r = ("packed", lib.g16_packed_a_bytes(M, K))
+        else:
+            ksplit = lib.g16_hgemm_plan(M, N, K, cus)
+            if ksplit > 1:
+                r = ("splitk", ksplit, lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit),
+                     lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit))
+            else:
+                r = ("plain",)
+        _remember(key, r)
+    return r
+
+
+def _remember(key: tuple, value: tuple) -> None:
+    if len(_routes) > 4096:  # bounded: shapes are few in practice
+        _routes.clear()
+    _routes[key] = value
+
+
 def _aligned(x: torch.Tensor) -> torch.Tensor:
     # The kernels read activations with 16-byte (rowscale) or dword (skinny) loads from a 16-byte
     # aligned base; supported() checks the weight only, as the reference does, so a misaligned
@@ -98,29 +128,35 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
     N = w_t.shape[1]
     dev = x2d.device
     stream = stream_handle(dev.index or 0)
-    cus = _sm_count(dev)
     b = None if bias is None else bias.float().contiguous()
     bptr = None if b is None else b.data_ptr()
 
     x2d = _aligned(x2d)
     if M <= SKINNY_MAX_M:  # memory-bound path, fp32 math
         out = torch.empty(M, N, device=dev, dtype=torch.float32)
-        ksplit = lib.g16_skinny_plan(M, N, K, cus)
-        bufs = split_buffers(dev, stream, lib.g16_skinny_workspace_bytes(M, N, K, ksplit),
-                             lib.g16_skinny_counter_bytes(M, N, K, ksplit))
+        key = (-M, N, K, dev.index or 0)
+        plan = _routes.get(key)
+        if plan is None:
+            ksplit = lib.g16_skinny_plan(M, N, K, _sm_count(dev))
+            plan = (ksplit, lib.g16_skinny_workspace_bytes(M, N, K, ksplit),
+                    lib.g16_skinny_counter_bytes(M, N, K, ksplit))
+            _remember(key, plan)
+        ksplit = plan[0]
+        bufs = split_buffers(dev, stream, plan[1], plan[2])
         fn = lib.g16_skinny_f32in if x2d.dtype == torch.float32 else lib.g16_skinny_f16in
         _clib.check(fn(x2d.data_ptr(), w_t.data_ptr(), out.data_ptr(), bptr, M, N, K, ksplit, *bufs, stream),
                     "skinny GEMM")
         return out if out_dtype == torch.float32 else out.to(out_dtype)
 
     # GEMM path: fp16 inputs, with per-row power-of-two scaling for rows that would overflow.
+    route = _gemm_route(lib, M, N, K, dev)
     rscale = torch.empty(M, device=dev, dtype=torch.float32)
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
     f32in = x2d.dtype == torch.float32
-    if lib.g16_hgemm_use_packed(M, N, K, cus):
+    if route[0] == "packed":
         # Large GEMM: the cast writes the fp16 copy straight into the tile-packed layout the
         # 256x256 kernel streams (same values, same result).
-        xp = torch.empty(lib.g16_packed_a_bytes(M, K) // 2, device=dev, dtype=torch.float16)
+        xp = torch.empty(route[1] // 2, device=dev, dtype=torch.float16)
         rs_fn = lib.g16_rowscale_pack_f32 if f32in else lib.g16_rowscale_pack_f16
         _clib.check(rs_fn(x2d.data_ptr(), xp.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
                     "rowscale cast")
@@ -134,11 +170,10 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
     _clib.check(rs_fn(x2d.data_ptr(), x16.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
                 "rowscale cast")
 
-    ksplit = lib.g16_hgemm_plan(M, N, K, cus)
-    if ksplit > 1:
+    if route[0] == "splitk":
         # Too few output tiles to fill the GPU: split K, reduce the slices in a fixed order.
-        bufs = split_buffers(dev, stream, lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit),
-                             lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit))
+        _, ksplit, pbytes, cbytes = route
+        bufs = split_buffers(dev, stream, pbytes, cbytes)
         st = lib.g16_hgemm_splitk(x16.data_ptr(), w_t.data_ptr(), out.data_ptr(),
                                   1 if out_dtype == torch.float16 else 0, bptr, rscale.data_ptr(),
                                   M, N, K, ksplit, *bufs, stream)
@@ -152,7 +187,7 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
 
 def prepacked_route(M: int, N: int, K: int, device: torch.device) -> bool:
     """True where mm_t takes the tile-packed 256x256 route, the one a prepacked weight serves."""
-    return bool(_clib.load().g16_hgemm_use_packed(M, N, K, _sm_count(device)))
+    return _gemm_route(_clib.load(), M, N, K, device)[0] == "packed"
 
 
 def pack_weight(w_t: torch.Tensor) -> torch.Tensor:
