@@ -11,9 +11,10 @@
 //     (64 lanes x 16 bytes = 512 fp16 columns), so every load is fully coalesced and the
 //     activation A[m,k] it multiplies is the same for the whole wavefront: A comes in through
 //     scalar loads, and the vector memory path carries nothing but B.
-//   * Each lane issues kU row loads before it uses any, so a workgroup has 128 KB of B in
-//     flight: enough to cover HBM latency with about one workgroup per CU. The weight is read
-//     exactly once, so the loads are non-temporal (measured 7-8 % faster at 4096x4096).
+//   * Each lane issues 16 (32 for M = 4) row loads before it uses any, so a workgroup has 128 KB
+//     (256 KB) of B in flight: enough to cover HBM latency with a workgroup on every other CU. The
+//     weight is read exactly once, so the loads are non-temporal (measured 7-8 % faster at
+//     4096x4096).
 //   * Reduction is fixed-order: the wavefronts' partial rows are added in wavefront order through
 //     LDS; when K is split over several workgroups, each slice publishes its 512 x M partial with
 //     device-coherent stores and the last slice to arrive (per strip) adds the slices in slice
@@ -27,7 +28,12 @@ namespace {
 constexpr int kStripCols = 512;  // 64 lanes x 8 fp16 columns
 constexpr int kWaves = 8;        // wavefronts per workgroup
 constexpr int kThreads = kWaves * kWave;
-constexpr int kU = 16;           // rows per wavefront per unrolled step
+constexpr int kMinRows = 8;      // the plan gives every wavefront at least this many rows
+
+// Rows each lane loads before using any (16 KB of B per wavefront at 16): 32 measured best for
+// M = 4 (13.0 vs 15.1 us at 4x4096x4096), 16 for M = 1, 2 and 8.
+template <int MM>
+constexpr int rows_in_flight() { return MM == 4 ? 32 : 16; }
 
 __device__ inline float x_at(const float* __restrict__ A, size_t i) { return A[i]; }
 // fp16 activations are read as the aligned dword holding them, so the (wavefront-uniform) load
@@ -75,27 +81,40 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     for (int j = 0; j < 8; ++j) acc[m][j] = 0.f;
 
   if (col < N) {
+    constexpr int U = rows_in_flight<MM>();
     const _Float16* bp = B + col;
     int k = k0;
-    for (; k + kU <= k1; k += kU) {
-      u32x4 w[kU];
+    for (; k + U <= k1; k += U) {
+      u32x4 w[U];
 #pragma unroll
-      for (int u = 0; u < kU; ++u)
+      for (int u = 0; u < U; ++u)
         w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(k + u) * N));
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
+      for (int u = 0; u < U; ++u) {
         float a[MM];
 #pragma unroll
         for (int m = 0; m < MM; ++m) a[m] = x_at(A, static_cast<size_t>(m) * K + k + u);
         fma_row<MM>(acc, a, w[u]);
       }
     }
-    for (; k < k1; ++k) {
-      const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(k) * N));
-      float a[MM];
+    if (k < k1) {
+      // Last, partial block: all U loads still go out together; rows past the slice re-read its last
+      // row and are not used (skipped, not multiplied by zero, so inf/NaN weights cannot leak in).
+      u32x4 w[U];
 #pragma unroll
-      for (int m = 0; m < MM; ++m) a[m] = x_at(A, static_cast<size_t>(m) * K + k);
-      fma_row<MM>(acc, a, w);
+      for (int u = 0; u < U; ++u) {
+        const int r = min(k + u, k1 - 1);
+        w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(r) * N));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (k + u < k1) {
+          float a[MM];
+#pragma unroll
+          for (int m = 0; m < MM; ++m) a[m] = x_at(A, static_cast<size_t>(m) * K + k + u);
+          fma_row<MM>(acc, a, w[u]);
+        }
+      }
     }
   }
 
@@ -224,13 +243,16 @@ int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, i
 }  // namespace g16
 
 extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
-  // About one 8-wavefront workgroup per CU (half that for M = 1, which measured faster: fewer, longer
-  // K slices mean a shorter split reduction), each wavefront streaming >= kU rows when K allows.
+  // One 8-wavefront workgroup per two CUs (measured faster than one per CU for M = 1..8: fewer,
+  // longer K slices make the split reduction shorter), each wavefront streaming >= kMinRows rows.
   if (N <= 0 || K <= 0 || num_cus <= 0) return 1;
   const int nstrips = g16::ceil_div(N, g16::kStripCols);
-  const int target = M == 1 ? (num_cus + 1) / 2 : num_cus;
+  const int target = (num_cus + 1) / 2;
   int ks = g16::ceil_div(target, nstrips);
-  const int cap = K / (g16::kWaves * g16::kU) > 1 ? K / (g16::kWaves * g16::kU) : 1;
+  // M = 1 keeps a full 16-row block per wavefront (6.3 vs 7.2 us at 1x1024x3072); larger M gain
+  // more from the extra slices than they lose to a partial block (10.8 vs 11.3 us at 4x1024x3072).
+  const int min_rows = M == 1 ? 16 : g16::kMinRows;
+  const int cap = K / (g16::kWaves * min_rows) > 1 ? K / (g16::kWaves * min_rows) : 1;
   ks = ks < 1 ? 1 : (ks > cap ? cap : ks);
   return g16::split_for(K, ks).ksplit;
 }

@@ -428,3 +428,29 @@ def test_packed_gemm_bitwise_equals_rowmajor(lib, cuda, M, K, N, out_dtype):
         assert torch.equal(c_pk, c_row)
     ref = oracle.gemm(_np(y16), _np(s), _np(w), _np(bias), "float16" if f16 else "float32")
     assert oracle.rel_err(_np(c_pk.float()), ref.astype(np.float64)) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_skinny_partial_block_ignores_rows_past_the_slice(lib, cuda, M):
+    # K=1024 with ksplit 16 gives each wavefront 8 rows, fewer than it loads at once: the last block
+    # re-reads the slice's last row for the missing ones and must not use them. A +inf in that last
+    # row must therefore reach the output as +inf (a 0 * inf from a reused row would make it NaN).
+    K, N, ksplit = 1024, 1024, 16
+    x = randn((M, K), seed=21).abs() + 0.5          # positive activations
+    w = randn((K, N), seed=22, scale=0.02, dtype=torch.float16)
+    w[7, 5] = float("inf")                          # last row of wavefront 0 of slice 0
+    w[1023, 9] = float("inf")                       # last row of the last slice
+    xd, wd = x.to(cuda), w.to(cuda)
+    out = torch.empty(M, N, device=cuda)
+    st = _stream(cuda)
+    ws, cnt = _split_bufs(lib.g16_skinny_workspace_bytes(M, N, K, ksplit), lib.g16_skinny_counter_bytes(M, N, K, ksplit), cuda)
+    assert lib.g16_skinny_f32in(xd.data_ptr(), wd.data_ptr(), out.data_ptr(), None, M, N, K, ksplit,
+                                ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), st) == 0
+    torch.cuda.synchronize()
+    y = _np(out)
+    assert np.isposinf(y[:, 5]).all() and np.isposinf(y[:, 9]).all()
+    finite = np.ones(N, dtype=bool)
+    finite[[5, 9]] = False
+    ref = oracle.skinny(_np(x), _np(w), None, "float32")
+    assert np.isfinite(y[:, finite]).all()
+    assert oracle.rel_err(y[:, finite], ref[:, finite]) <= SKINNY_TOL
