@@ -58,7 +58,10 @@ __device__ inline lds_short4v* as_lds4(const unsigned char* p) { return (lds_sho
 // cannot tell apart from the stage being read (it would wait for the DMA before every LDS
 // read); the kernel waits for its DMA explicitly (vmcnt 0) before the barrier that publishes a
 // stage. Vector memory returns in order, so the compiler's own vmcnt waits stay correct (they can
-// only wait longer) with these loads in flight.
+// only wait longer) with these loads in flight. M0 (the LDS base of the DMA) is set and consumed
+// inside the same statement; clang warns that m0 is reserved, but these kernels contain no other
+// reader of M0 (no LDS-direct, GWS or message instructions): in the generated assembly every
+// `s_mov_b32 m0` is one of these statements, immediately followed by its DMA.
 __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, const unsigned char* lds, uint32_t off) {
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds));
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
