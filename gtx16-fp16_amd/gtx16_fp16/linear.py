@@ -34,8 +34,9 @@ class FastLinear(nn.Module):
     def __init__(self, in_features: int, out_features: int, bias: bool = True, device=None):
         super().__init__()
         self.in_features, self.out_features = in_features, out_features
-        # (M, device index) -> (PreparedLaunch, ksplit, (partial, counter) bytes, weight pointer), or None when
-        # the weight is not supported by the kernels (token-by-token fast path).
+        # (M, device index) -> (PreparedLaunch or None, ksplit, (partial, counter) bytes, weight pointer,
+        # bias pointer) for the token-by-token fast path; None in the first field when the weight or
+        # bias the pointers name cannot be handed to the kernel (the call then takes the general path).
         self._skinny: dict = {}
         # prepacked weight for the large-GEMM route and the (pointer, version) of weight_t it was built from
         self._wp: torch.Tensor | None = None
@@ -60,19 +61,24 @@ class FastLinear(nn.Module):
 
     def _decode_entry(self, M: int, dev: torch.device):
         key = (M, dev.index)
-        w = self.weight_t
-        entry = self._skinny.get(key, False)
-        if entry is False or (entry is not None and entry[3] != w.data_ptr()):
+        w, b = self.weight_t, self.bias
+        bptr = None if b is None else b.data_ptr()
+        entry = self._skinny.get(key)
+        if entry is None or entry[3] != w.data_ptr() or entry[4] != bptr:
+            # (re)validated whenever weight_t or bias is a different tensor, e.g. after .to() or
+            # .half() (which turns the bias fp16: the kernel reads an fp32 bias)
             K, N = self.in_features, self.out_features
             ok = (w.dtype == torch.float16 and w.is_contiguous() and w.device == dev and K % 8 == 0
-                  and N % 8 == 0 and w.data_ptr() % 16 == 0 and _is_target(dev.index or 0))
-            entry = None
+                  and N % 8 == 0 and w.data_ptr() % 16 == 0 and _is_target(dev.index or 0)
+                  and (b is None or (b.dtype == torch.float32 and b.device == dev and b.is_contiguous()
+                                     and b.numel() == N)))
+            pl, ksplit, sizes = None, 0, (0, 0)
             if ok:
                 lib = _clib.load()
                 ksplit = lib.g16_skinny_plan(M, N, K, _sm_count(dev))
-                entry = (PreparedLaunch(lib.g16_skinny_f32in, "skinny GEMM"), ksplit,
-                         (lib.g16_skinny_workspace_bytes(M, N, K, ksplit), lib.g16_skinny_counter_bytes(M, N, K, ksplit)),
-                         w.data_ptr())
+                pl = PreparedLaunch(lib.g16_skinny_f32in, "skinny GEMM")
+                sizes = (lib.g16_skinny_workspace_bytes(M, N, K, ksplit), lib.g16_skinny_counter_bytes(M, N, K, ksplit))
+            entry = (pl, ksplit, sizes, w.data_ptr(), bptr)
             self._skinny[key] = entry
         return entry
 
@@ -97,21 +103,19 @@ class FastLinear(nn.Module):
             M = x.numel() // K if shape[-1] == K else -1
             if 0 < M <= SKINNY_MAX_M:
                 dev = x.device
-                entry = self._decode_entry(M, dev)
-                if entry is not None:
-                    pl, ksplit, sizes, wptr = entry
+                pl, ksplit, sizes, wptr, bptr = self._decode_entry(M, dev)
+                if pl is not None:
                     stream = stream_handle(dev.index or 0)
                     bufs = split_buffers(dev, stream, *sizes)
                     out = torch.empty(*shape[:-1], N, device=dev, dtype=torch.float32)
-                    pl(x.data_ptr(), wptr, out.data_ptr(), None if self.bias is None else self.bias.data_ptr(),
-                       M, N, K, ksplit, *bufs, stream)
+                    pl(x.data_ptr(), wptr, out.data_ptr(), bptr, M, N, K, ksplit, *bufs, stream)
                     return out
         x2 = x.reshape(-1, self.in_features)
         if x2.dtype not in (torch.float16, torch.float32):
             x2 = x2.float()
         x2 = x2.contiguous()  # fp32 stays fp32: the kernels cast (and rescale large rows) themselves
         if x2.shape[0] == 0 or not supported(x2, self.weight_t):
-            y = F.linear(x2.float(), self.weight_t.t().float(), self.bias)
+            y = F.linear(x2.float(), self.weight_t.t().float(), None if self.bias is None else self.bias.float())
         else:
             odt = torch.float32 if out_dtype == torch.float32 else torch.float16
             M = x2.shape[0]

@@ -106,10 +106,30 @@ def _remember(key: tuple, value: tuple) -> None:
     _routes[key] = value
 
 
+def _check_operands(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None) -> None:
+    # The reference leaves validation to supported() (ops.py:29-35, "Check supported() first"); a
+    # call that skips it must still not hand the kernels a pointer they cannot read (a bias or
+    # weight on another device, a misaligned weight), so those are rejected here.
+    if not (x2d.is_cuda and x2d.dim() == 2 and x2d.dtype in (torch.float16, torch.float32)):
+        raise ValueError("mm_t: x2d must be a 2-D fp16 or fp32 CUDA tensor")
+    if not (w_t.dim() == 2 and w_t.dtype == torch.float16 and w_t.device == x2d.device and w_t.is_contiguous()
+            and w_t.data_ptr() % 16 == 0):
+        raise ValueError("mm_t: w_t must be a contiguous, 16-byte aligned fp16 tensor on x2d's device")
+    K, N = w_t.shape
+    if x2d.shape[1] != K or K % 8 or N % 8:
+        raise ValueError(f"mm_t: shapes x2d {tuple(x2d.shape)} and w_t {tuple(w_t.shape)} are not supported "
+                         "(K and N must match and be multiples of 8)")
+    if bias is not None and (bias.device != x2d.device or bias.numel() != N):
+        raise ValueError(f"mm_t: bias must hold {N} values on x2d's device")
+
+
 def _aligned(x: torch.Tensor) -> torch.Tensor:
-    # The kernels read activations with 16-byte (rowscale) or dword (skinny) loads from a 16-byte
-    # aligned base; supported() checks the weight only, as the reference does, so a misaligned
-    # activation view is copied into a fresh allocation.
+    # The kernels read activations as M*K contiguous values with 16-byte (rowscale) or dword
+    # (skinny) loads from a 16-byte aligned base; supported() checks the weight's alignment only,
+    # as the reference does, so a misaligned or non-contiguous activation view (an expanded one
+    # may own fewer than M*K values) is copied into a fresh allocation.
+    if not x.is_contiguous():
+        return x.contiguous()
     return x if x.data_ptr() % 16 == 0 else x.clone()
 
 
@@ -123,6 +143,7 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
     scaled back; shapes with too few output tiles split K with a deterministic reduction."""
     if out_dtype not in (torch.float32, torch.float16):
         raise ValueError(f"out_dtype must be float32 or float16, got {out_dtype}")
+    _check_operands(x2d, w_t, bias)
     lib = _clib.load()
     M, K = x2d.shape
     N = w_t.shape[1]
@@ -193,6 +214,10 @@ def prepacked_route(M: int, N: int, K: int, device: torch.device) -> bool:
 def pack_weight(w_t: torch.Tensor) -> torch.Tensor:
     """w_t [K, N] fp16 (CUDA, contiguous, K and N multiples of 8) -> its prepacked form for
     mm_t_prepacked: w_t transposed into the GEMM's tile-packed layout, a 1-D fp16 tensor."""
+    if not (w_t.is_cuda and w_t.dim() == 2 and w_t.dtype == torch.float16 and w_t.is_contiguous()
+            and w_t.data_ptr() % 16 == 0 and w_t.shape[0] % 8 == 0 and w_t.shape[1] % 8 == 0):
+        raise ValueError("pack_weight: w_t must be a contiguous, 16-byte aligned fp16 CUDA tensor "
+                         "with both dimensions multiples of 8")
     lib = _clib.load()
     K, N = w_t.shape
     wp = torch.empty(lib.g16_packed_b_bytes(K, N) // 2, device=w_t.device, dtype=torch.float16)
@@ -209,6 +234,7 @@ def mm_t_prepacked(x2d: torch.Tensor, w_t: torch.Tensor, wp: torch.Tensor, bias:
     exactly mm_t. Check supported(x2d, w_t) first."""
     if out_dtype not in (torch.float32, torch.float16):
         raise ValueError(f"out_dtype must be float32 or float16, got {out_dtype}")
+    _check_operands(x2d, w_t, bias)
     M, K = x2d.shape
     N = w_t.shape[1]
     dev = x2d.device

@@ -41,6 +41,17 @@ def test_mm_t_rejects_bad_out_dtype_before_any_device_work():
         g.mm_t(torch.randn(4, 8), torch.randn(8, 8).half(), None, torch.bfloat16)
 
 
+def test_mm_t_and_pack_weight_reject_host_tensors():
+    # without supported() in front, a host tensor must be refused before any pointer reaches a kernel
+    x, w = torch.randn(16, 64), torch.randn(64, 32).half()
+    with pytest.raises(ValueError, match="x2d"):
+        g.mm_t(x, w)
+    with pytest.raises(ValueError, match="x2d"):
+        ops.mm_t_prepacked(x, w, torch.empty(0, dtype=torch.float16))
+    with pytest.raises(ValueError, match="pack_weight"):
+        ops.pack_weight(w)
+
+
 def test_matmul_fallback_for_odd_shapes():
     # tests/test_correctness.py:62-66 (CPU tensors always take the fallback)
     a = torch.randn(33, 13).half()

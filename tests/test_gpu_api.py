@@ -56,6 +56,26 @@ def test_fast_linear_is_deterministic_across_calls(g, cuda):
         assert torch.equal(o, outs[0])
 
 
+def test_fast_linear_decode_after_half_and_bias_swap(g, cuda):
+    # .half() makes the bias buffer fp16 and replaces it: the token-by-token path must notice the
+    # new tensor and not hand its pointer to a kernel that reads an fp32 bias
+    torch.manual_seed(0)
+    fl = g.FastLinear.from_linear(nn.Linear(1024, 768).to(cuda))
+    x = torch.randn(2, 1024, device=cuda)
+    with torch.no_grad():
+        fl(x)
+        fl.half()
+        assert fl.bias.dtype == torch.float16 and fl.weight_t.dtype == torch.float16
+        y = fl(x)
+        torch.cuda.synchronize()
+        assert oracle.rel_err(y.cpu().numpy(), _ref_linear(x, fl)) <= 1e-5
+        fl.bias = torch.randn(768, device=cuda)          # a new fp32 bias: the fast path again
+        y2 = fl(x)
+        torch.cuda.synchronize()
+        assert fl._decode_entry(2, x.device)[0] is not None
+        assert oracle.rel_err(y2.cpu().numpy(), _ref_linear(x, fl)) <= 1e-5
+
+
 def test_fast_linear_falls_back_when_grad_needed(g, cuda):
     fl = g.FastLinear.from_linear(nn.Linear(256, 256).to(cuda))
     x = torch.randn(4, 256, device=cuda, requires_grad=True)
@@ -105,6 +125,16 @@ def test_bias_and_inputs_are_not_modified(g, cuda, M):
         g.mm_t(x, w, b, torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(x, x0) and torch.equal(w, w0) and torch.equal(b, b0)
+
+
+@pytest.mark.parametrize("M", [4, 64, 600])
+def test_mm_t_on_non_contiguous_views(g, cuda, M):
+    # an expanded view owns only K values and a transposed one has row stride 1: both are copied
+    # to a contiguous buffer before a kernel reads M*K contiguous values
+    w = torch.randn(512, 256, device=cuda).half()
+    for x in (torch.randn(1, 512, device=cuda).expand(M, 512), torch.randn(512, M, device=cuda).t()):
+        assert not x.is_contiguous()
+        assert torch.equal(g.mm_t(x, w), g.mm_t(x.contiguous(), w))
 
 
 def test_matmul_fp16_drop_in(g, cuda):

@@ -74,6 +74,23 @@ def test_mm_t_prepacked_rejects_a_wrong_packed_weight(ops, cuda):
         ops.mm_t_prepacked(x, w, torch.empty(16, dtype=torch.float16, device=cuda))
 
 
+def test_mm_t_rejects_operands_the_kernels_cannot_read(ops, cuda):
+    # a bias or weight on another device, or a misaligned weight view, raises instead of launching
+    x = torch.randn(64, 256, device=cuda)
+    w = torch.randn(256, 128, device=cuda).half()
+    with pytest.raises(ValueError, match="bias"):
+        ops.mm_t(x, w, torch.zeros(128))
+    with pytest.raises(ValueError, match="bias"):
+        ops.mm_t(x, w, torch.zeros(64, device=cuda))
+    with pytest.raises(ValueError, match="w_t"):
+        ops.mm_t(x, w.cpu())
+    wide = torch.randn(256 * 128 + 4, device=cuda).half()
+    with pytest.raises(ValueError, match="w_t"):
+        ops.mm_t(x, wide[4:].view(256, 128))   # 8-byte aligned base
+    with pytest.raises(ValueError, match="pack_weight"):
+        ops.pack_weight(wide[4:].view(256, 128))
+
+
 def test_fast_linear_large_batch_uses_prepacked_weight_and_tracks_changes(cuda):
     import gtx16_fp16 as g
     from gtx16_fp16 import ops
