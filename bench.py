@@ -317,27 +317,36 @@ def bench_overhead(torch, g, dev, n: int = 1000) -> list:
 
 def bench_peak(torch, lib, dev) -> list:
     """Instruction and HBM peaks of this part (the analogue of the reference's bench/peak.py):
-    fp32 FMA, packed fp16 FMA and the two fp16 MFMA shapes from register-only loops, and a
-    streaming read of a 4 GiB buffer. Each is the best of 3 timed launches after a warm-up."""
+    fp32 FMA, packed fp16 FMA and the two fp16 MFMA shapes from register-only loops (the MFMA ones
+    on near-constant and on random operand bits), and a streaming read of a 4 GiB buffer. Each is
+    the best of 3 timed launches after a warm-up; the instruction peaks also report the shader
+    clock their loop ran at (s_memtime cycles over 100 MHz reference ticks)."""
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     stream = torch.cuda.current_stream(dev).cuda_stream
     rows = []
-    for kind, name, waves_per_simd, iters in ((0, "fp32 FMA (VALU)", 8, 20000), (1, "packed fp16 FMA (VALU)", 8, 20000),
-                                              (2, "MFMA f16 32x32x16", 2, 20000), (3, "MFMA f16 16x16x32", 2, 20000)):
+    clocks = torch.zeros(2, dtype=torch.int64, device=dev)
+    for kind, name, waves_per_simd, iters in (
+            (0, "fp32 FMA (VALU)", 8, 20000), (1, "packed fp16 FMA (VALU)", 8, 20000),
+            (2, "MFMA f16 32x32x16", 2, 20000), (3, "MFMA f16 16x16x32", 2, 20000),
+            (4, "MFMA f16 32x32x16, random operands", 2, 20000), (5, "MFMA f16 16x16x32, random operands", 2, 20000)):
         blocks = cus * waves_per_simd  # 256-lane workgroups: 4 wavefronts each, one per SIMD
         out = torch.empty(blocks * 256, device=dev)
         _clib_ok(lib.g16_peak_run(kind, blocks, 100, out.data_ptr(), stream))
         torch.cuda.synchronize()
-        best = float("inf")
+        best, mhz = float("inf"), 0.0
         for _ in range(3):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            _clib_ok(lib.g16_peak_run(kind, blocks, iters, out.data_ptr(), stream))
+            _clib_ok(lib.g16_peak_run_clocked(kind, blocks, iters, out.data_ptr(), clocks.data_ptr(), stream))
             e1.record()
             e1.synchronize()
-            best = min(best, e0.elapsed_time(e1) * 1e-3)
+            t = e0.elapsed_time(e1) * 1e-3
+            if t < best:
+                cyc, ticks = clocks.tolist()
+                best, mhz = t, (100.0 * cyc / ticks if ticks else 0.0)
         flop = lib.g16_peak_flops_per_lane_iter(kind) * blocks * 256 * iters
-        rows.append({"peak": name, "TFLOP/s": round(flop / best / 1e12, 1), "ms": round(best * 1e3, 3)})
+        rows.append({"peak": name, "TFLOP/s": round(flop / best / 1e12, 1), "ms": round(best * 1e3, 3),
+                     "clock_MHz": round(mhz)})
         print(json.dumps(rows[-1]), flush=True)
     nbytes = 4 << 30
     buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)

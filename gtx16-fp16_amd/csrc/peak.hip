@@ -6,9 +6,15 @@
 //   kind 1: packed fp16 FMA (v_pk_fma_f16), 8 chains of half2 per lane;
 //   kind 2: v_mfma_f32_32x32x16_f16, 8 independent accumulators per wavefront;
 //   kind 3: v_mfma_f32_16x16x32_f16, 16 independent accumulators per wavefront;
+//   kinds 4, 5: kinds 2, 3 with operands of random fp16 bit patterns instead of the near-constant
+//           ones of kinds 2, 3. The MFMA datapath's power depends on how many operand bits toggle,
+//           and the part lowers its clock to hold its power limit, so these give the rate a GEMM
+//           on real data can reach; 2 and 3 give the rate at the part's top clock.
 // and a streaming read of a large buffer (16-byte loads, grid-stride) for HBM bandwidth.
 // Everything stays in registers except the read stream; results are folded into `out` so the
-// compiler cannot drop the work.
+// compiler cannot drop the work. Workgroup 0's first wavefront can also report the shader clock
+// cycles and the 100 MHz reference ticks its loop took (s_memtime, s_memrealtime), which give the
+// clock the part held.
 #include "g16_common.hpp"
 
 namespace g16 {
@@ -16,20 +22,51 @@ namespace {
 
 typedef _Float16 half2x __attribute__((ext_vector_type(2)));
 
-__global__ __launch_bounds__(256) void peak_ffma(float* out, float a, float b, int iters) {
+// Loop clock of workgroup 0, wavefront 0: {shader cycles, 100 MHz reference ticks} -> clk[0..1].
+struct LoopClock {
+  unsigned long long c0 = 0, r0 = 0;
+  __device__ void start() {
+    c0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  __device__ void stop(unsigned long long* clk) const {
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    if (clk != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+      clk[0] = c1 - c0;
+      clk[1] = r1 - r0;
+    }
+  }
+};
+
+// Random fp16 bit pattern: random sign and 10 mantissa bits, exponent in [2^-3, 2^0) so that
+// 20000 accumulations of 16-term products stay far from overflow.
+__device__ inline _Float16 random_half(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  const uint16_t bits = static_cast<uint16_t>((x & 0x83ffu) | ((12u + ((x >> 10) & 3u)) << 10));
+  return __builtin_bit_cast(_Float16, bits);
+}
+
+__global__ __launch_bounds__(256) void peak_ffma(float* out, unsigned long long* clk, float a, float b, int iters) {
   float x[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(threadIdx.x + i);
+  LoopClock lc;
+  lc.start();
   for (int it = 0; it < iters; ++it)
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = fmaf(x[i], a, b);
+  lc.stop(clk);
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) s += x[i];
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-__global__ __launch_bounds__(256) void peak_hfma2(float* out, float af, float bf, int iters) {
+__global__ __launch_bounds__(256) void peak_hfma2(float* out, unsigned long long* clk, float af, float bf, int iters) {
   const half2x a = {static_cast<_Float16>(af), static_cast<_Float16>(af)};
   const half2x b = {static_cast<_Float16>(bf), static_cast<_Float16>(bf)};
   half2x x[8];
@@ -38,47 +75,61 @@ __global__ __launch_bounds__(256) void peak_hfma2(float* out, float af, float bf
     const _Float16 v = static_cast<_Float16>((threadIdx.x + i) * 1e-3f);
     x[i] = half2x{v, v};
   }
+  LoopClock lc;
+  lc.start();
   for (int it = 0; it < iters; ++it)
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = x[i] * a + b;
+  lc.stop(clk);
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) s += static_cast<float>(x[i].x) + static_cast<float>(x[i].y);
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-__global__ __launch_bounds__(256) void peak_mfma32(float* out, float seed, int iters) {
+// MFMA operands: near-constant (a depends on the lane, b on the element only) or random bits
+template <bool RANDOM>
+__device__ inline void mfma_operands(half8& a, half8& b, float seed) {
+  const uint32_t g = (blockIdx.x * blockDim.x + threadIdx.x) * 16u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = RANDOM ? random_half(g + i) : static_cast<_Float16>(seed * (threadIdx.x + i));
+    b[i] = RANDOM ? random_half(g + 8 + i) : static_cast<_Float16>(seed * i);
+  }
+}
+
+template <bool RANDOM>
+__global__ __launch_bounds__(256) void peak_mfma32(float* out, unsigned long long* clk, float seed, int iters) {
   float16v acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = float16v{};
   half8 a, b;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = static_cast<_Float16>(seed * (threadIdx.x + i));
-    b[i] = static_cast<_Float16>(seed * i);
-  }
+  mfma_operands<RANDOM>(a, b, seed);
+  LoopClock lc;
+  lc.start();
   for (int it = 0; it < iters; ++it)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+  lc.stop(clk);
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) s += acc[i][threadIdx.x & 15];
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-__global__ __launch_bounds__(256) void peak_mfma16(float* out, float seed, int iters) {
+template <bool RANDOM>
+__global__ __launch_bounds__(256) void peak_mfma16(float* out, unsigned long long* clk, float seed, int iters) {
   float4v acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
   half8 a, b;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = static_cast<_Float16>(seed * (threadIdx.x + i));
-    b[i] = static_cast<_Float16>(seed * i);
-  }
+  mfma_operands<RANDOM>(a, b, seed);
+  LoopClock lc;
+  lc.start();
   for (int it = 0; it < iters; ++it)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i], 0, 0, 0);
+  lc.stop(clk);
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) s += acc[i][threadIdx.x & 3];
@@ -113,25 +164,32 @@ extern "C" double g16_peak_flops_per_lane_iter(int kind) {
   switch (kind) {
     case 0: return 8.0 * 2;                          // 8 fp32 FMAs
     case 1: return 8.0 * 2 * 2;                      // 8 packed fp16 FMAs
-    case 2: return 8.0 * 32 * 32 * 16 * 2 / 64;      // 8 MFMA 32x32x16
-    case 3: return 16.0 * 16 * 16 * 32 * 2 / 64;     // 16 MFMA 16x16x32
+    case 2: case 4: return 8.0 * 32 * 32 * 16 * 2 / 64;      // 8 MFMA 32x32x16
+    case 3: case 5: return 16.0 * 16 * 16 * 32 * 2 / 64;     // 16 MFMA 16x16x32
     default: return 0.0;
   }
 }
 
-extern "C" int g16_peak_run(int kind, int blocks, int iters, float* out, void* stream) {
-  // out must hold blocks * 256 floats
+extern "C" int g16_peak_run_clocked(int kind, int blocks, int iters, float* out, unsigned long long* clocks,
+                                    void* stream) {
+  // out must hold blocks * 256 floats; clocks (may be NULL) receives 2 values
   if (blocks <= 0 || iters < 0) return G16_E_SHAPE;
   if (out == nullptr) return G16_E_NULL;
   const dim3 grid(static_cast<unsigned>(blocks)), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (kind) {
-    case 0: return g16::launch(g16::peak_ffma, grid, block, s, out, 0.999f, 0.001f, iters);
-    case 1: return g16::launch(g16::peak_hfma2, grid, block, s, out, 0.999f, 0.001f, iters);
-    case 2: return g16::launch(g16::peak_mfma32, grid, block, s, out, 1e-3f, iters);
-    case 3: return g16::launch(g16::peak_mfma16, grid, block, s, out, 1e-3f, iters);
+    case 0: return g16::launch(g16::peak_ffma, grid, block, s, out, clocks, 0.999f, 0.001f, iters);
+    case 1: return g16::launch(g16::peak_hfma2, grid, block, s, out, clocks, 0.999f, 0.001f, iters);
+    case 2: return g16::launch(g16::peak_mfma32<false>, grid, block, s, out, clocks, 1e-3f, iters);
+    case 3: return g16::launch(g16::peak_mfma16<false>, grid, block, s, out, clocks, 1e-3f, iters);
+    case 4: return g16::launch(g16::peak_mfma32<true>, grid, block, s, out, clocks, 1e-3f, iters);
+    case 5: return g16::launch(g16::peak_mfma16<true>, grid, block, s, out, clocks, 1e-3f, iters);
     default: return G16_E_DTYPE;
   }
+}
+
+extern "C" int g16_peak_run(int kind, int blocks, int iters, float* out, void* stream) {
+  return g16_peak_run_clocked(kind, blocks, iters, out, nullptr, stream);
 }
 
 extern "C" int g16_stream_read(const void* buf, size_t bytes, int blocks, float* out, void* stream) {

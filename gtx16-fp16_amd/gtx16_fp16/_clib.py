@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before libg16.so)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libg16.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -50,6 +50,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_skinny_plan": (_I, [_I, _I, _I, _I]),
     "g16_peak_flops_per_lane_iter": (ctypes.c_double, [_I]),
     "g16_peak_run": (_I, [_I, _I, _I, _P, _P]),
+    "g16_peak_run_clocked": (_I, [_I, _I, _I, _P, _P, _P]),
     "g16_stream_read": (_I, [_P, _SZ, _I, _P, _P]),
 }
 

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 5
+#define G16_ABI_VERSION 6
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -160,14 +160,19 @@ int g16_skinny_plan(int M, int N, int K, int num_cus);
  * Peak microbenchmark: the MI355X counterpart of the reference's bench/peak.py:1-63 (which times
  * FFMA, HFMA2 and mma.sync kernels). No counterpart in the kernel ABI: it measures the instruction
  * and bandwidth peaks the benchmark's rooflines divide by, at the clocks the part holds.
- * kind 0: fp32 FMA (VALU); 1: packed fp16 FMA; 2: MFMA 32x32x16 f16; 3: MFMA 16x16x32 f16.
+ * kind 0: fp32 FMA (VALU); 1: packed fp16 FMA; 2: MFMA 32x32x16 f16; 3: MFMA 16x16x32 f16;
+ * 4, 5: kinds 2, 3 on random fp16 operand bits (the MFMA power, hence the clock the part holds,
+ * depends on operand toggling: 2 and 3 run at the top clock, 4 and 5 at the clock real data gets).
  * g16_peak_run launches `blocks` workgroups of 256 lanes looping `iters` times; each lane does
  * g16_peak_flops_per_lane_iter(kind) flops per iteration. `out` holds blocks * 256 floats.
+ * g16_peak_run_clocked does the same and, when `clocks` is not NULL, stores into clocks[0] the
+ * shader clock cycles and into clocks[1] the 100 MHz reference ticks of workgroup 0's loop.
  * g16_stream_read reads `bytes` (a multiple of 16, 16-byte aligned buffer) once with 16-byte
  * loads from `blocks` workgroups of 256 lanes; `out` holds blocks * 256 floats.
  */
 double g16_peak_flops_per_lane_iter(int kind);
 int g16_peak_run(int kind, int blocks, int iters, float* out, void* stream);
+int g16_peak_run_clocked(int kind, int blocks, int iters, float* out, unsigned long long* clocks, void* stream);
 int g16_stream_read(const void* buf, size_t bytes, int blocks, float* out, void* stream);
 
 #ifdef __cplusplus

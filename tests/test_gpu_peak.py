@@ -16,7 +16,7 @@ def lib(cuda):
     return _clib.load()
 
 
-@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4, 5])
 def test_peak_kernels_run(lib, cuda, kind):
     blocks = 8
     out = torch.full((blocks * 256,), float("nan"), device=cuda)
@@ -25,6 +25,21 @@ def test_peak_kernels_run(lib, cuda, kind):
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
     assert lib.g16_peak_flops_per_lane_iter(kind) > 0
+
+
+@pytest.mark.parametrize("kind", [0, 4])
+def test_peak_clock_readout(lib, cuda, kind):
+    # workgroup 0's loop: shader cycles and 100 MHz reference ticks give a clock in the part's range
+    blocks, iters = 8, 20000
+    out = torch.empty(blocks * 256, device=cuda)
+    clocks = torch.zeros(2, dtype=torch.int64, device=cuda)
+    st = torch.cuda.current_stream(cuda).cuda_stream
+    assert lib.g16_peak_run_clocked(kind, blocks, iters, out.data_ptr(), clocks.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    cyc, ticks = clocks.tolist()
+    assert cyc > 0 and ticks > 0
+    assert 300.0 < 100.0 * cyc / ticks < 3500.0
+    assert torch.isfinite(out).all()
 
 
 def test_peak_fp32_fma_value(lib, cuda):
