@@ -8,9 +8,12 @@
 //
 // Structure:
 //   * A workgroup owns a BM x BN output tile; each wavefront owns a (BM/WGM) x (BN/WGN) sub-tile
-//     made of 32x32 blocks computed with v_mfma_f32_32x32x16_f16 (fp32 accumulators). The large
-//     tile is 256x256 with 8 wavefronts (two per SIMD); smaller tiles (128x128, 64x128, 32x128)
-//     use 4 wavefronts and serve small M and split-K.
+//     made of MFMA blocks with fp32 accumulators. The large tile is 256x256 with 8 wavefronts (two
+//     per SIMD) on 16x16 blocks of v_mfma_f32_16x16x32_f16; smaller tiles (128x128, 64x128,
+//     32x128) use 4 wavefronts on 32x32 blocks of v_mfma_f32_32x32x16_f16 and serve small M and
+//     split-K. Both instructions have the same peak rate; on random operands the 16x16x32 one
+//     draws less power, and at 4096^3 the part is power-limited (it holds ~1.6 GHz, not 2.4), so
+//     the large tile runs 4-6 % faster with it.
 //   * K advances in steps of BK through a ring of NSTAGE LDS stages filled by DMA
 //     (buffer_load_dwordx4 ... lds), so operand tiles never pass through registers. Lanes whose
 //     16-byte chunk lies outside the matrix (ragged M, N, K or a split-K slice boundary) are given
@@ -19,11 +22,11 @@
 //     layout is chosen through which global chunk each lane fetches: A is stored [row][k], B
 //     [k][n] like the weight, each with a 16-byte-chunk XOR swizzle (swz_a, swz_b) that keeps the
 //     fragment reads free of bank conflicts.
-//   * MFMA operands need K-contiguous runs per lane. A fragments are one 16-byte LDS read each.
-//     B fragments use the gfx950 transposing read ds_read_b64_tr_b16: within each 16-lane group,
-//     lane p receives element p%4 of the 8-byte pieces addressed by lanes p/4 + 4j (j = 0..3), so
-//     pointing lane q at B[k0 + q/4][n0 + 4(q%4)] hands lane p the run B[k0..k0+3][n0 + p]; two
-//     such reads give the 8-deep run one operand needs.
+//   * MFMA operands need K-contiguous runs per lane (8 halves). A fragments are one 16-byte LDS
+//     read each. B fragments use the gfx950 transposing read ds_read_b64_tr_b16: within each
+//     16-lane group, lane p receives element p%4 of the 8-byte pieces addressed by lanes p/4 + 4j
+//     (j = 0..3), so pointing lane q at B[k0 + q/4][n0 + 4(q%4)] hands lane p the run
+//     B[k0..k0+3][n0 + p]; two such reads give the 8-deep run one operand needs.
 //   * Schedules: the 8-wavefront tile runs a ping-pong between the two wavefronts of each SIMD
 //     (one issues a step's MFMAs while the other reads LDS and issues DMA, swapping at every
 //     barrier); the 4-wavefront tiles interleave DMA, MFMAs and the next step's fragment reads
@@ -37,6 +40,8 @@
 //     device-coherent stores); the last slice to arrive adds all slices in slice order and runs the
 //     epilogue. Deterministic, and bias/scale/cast are fused (the reference prefills C with the bias
 //     and adds with fp32 atomics, kernels.py:119-122, ops.py:54-62).
+#include <type_traits>
+
 #include "g16_common.hpp"
 
 namespace g16 {
@@ -70,14 +75,21 @@ __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, const unsigned char* l
                : "memory", "m0");
 }
 
-template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int NSTAGE_>
+template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int NSTAGE_, bool MF16_ = false>
 struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, NSTAGE = NSTAGE_;
   static constexpr int WAVES = WGM * WGN;
   static constexpr int THREADS = WAVES * kWave;
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;  // wavefront sub-tile
-  static constexpr int TM = WTM / 32, TN = WTN / 32;      // 32x32 MFMA blocks per wavefront
-  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 blocks");
+  // MFMA shape: v_mfma_f32_16x16x32_f16 (MF16) or v_mfma_f32_32x32x16_f16. Same flops per cycle;
+  // on random operands the 16x16x32 form draws less power, so a power-limited part holds a higher
+  // clock with it (measured: +3 to +8 % per GEMM step at the same LDS traffic).
+  static constexpr bool MF16 = MF16_;
+  static constexpr int MB = MF16 ? 16 : 32;               // MFMA output block edge
+  static constexpr int MK = MF16 ? 32 : 16;               // MFMA K depth
+  static constexpr int TM = WTM / MB, TN = WTN / MB;      // MFMA blocks per wavefront
+  static_assert(TM >= 1 && TN >= 1 && WTM % MB == 0 && WTN % MB == 0, "whole MFMA blocks");
+  static_assert(!MF16 || (TM % 2 == 0 && TN % 2 == 0), "the epilogue stores 2x2 groups of 16x16 blocks");
   static_assert(BK == 32 || BK == 64, "K step");
   static constexpr int A_BYTES = BM * BK * 2;            // one stage of A
   static constexpr int B_BYTES = BK * BN * 2;            // one stage of B
@@ -94,7 +106,7 @@ struct TileCfg {
   static_assert(NSTAGE >= 3 && (NSTAGE - 2) * DMA_PER_STEP <= 63, "vmcnt range");
 };
 
-using Cfg256 = TileCfg<256, 256, 32, 2, 4, 4>;  // 8 wavefronts (two per SIMD), 4-stage ring, 128 KB
+using Cfg256 = TileCfg<256, 256, 32, 2, 4, 4, true>;  // 8 wavefronts (two per SIMD), 4-stage ring, 128 KB
 using Cfg128 = TileCfg<128, 128, 32, 2, 2, 4>;  // 64 KB: two workgroups per CU
 using Cfg64 = TileCfg<64, 128, 64, 1, 4, 3>;
 using Cfg32 = TileCfg<32, 128, 64, 1, 4, 3>;
@@ -126,7 +138,8 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
                                                          const float* __restrict__ rscale, float* __restrict__ part,
                                                          uint32_t* __restrict__ counters, int M, int N, int K,
                                                          int kchunk, int ksplit, int ntm, int ntn) {
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN, MB = Cfg::MB, MK = Cfg::MK;
+  static_assert(!(SPLITK && Cfg::MF16), "split-K publishes 32x32-block accumulators");
   constexpr int BK = Cfg::BK, NSTAGE = Cfg::NSTAGE;
   __shared__ __attribute__((aligned(1024))) unsigned char sA[NSTAGE][Cfg::A_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char sB[NSTAGE][Cfg::B_BYTES];
@@ -217,33 +230,38 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   };
 
   // ---- fragment addressing (byte offsets within a stage) ----
-  const int frow = lane & 31;  // A fragment row within a 32-block
-  const int fk = lane >> 5;    // which 8-run of the 16-wide K step
-  // B transposed reads: 16-lane group g covers columns +16*(g&1), k rows +8*(g>>1); lane q of the
-  // group addresses row q/4, columns 4*(q%4).
+  // MFMA operands (both shapes): lane l holds the 8-deep k-run 8*(l/MB) .. +7 of the MFMA's K step
+  // for A row l%MB (B column l%MB). A and B use the same lane -> k assignment, so the product does
+  // not depend on how the instruction orders k internally.
+  const int frow = lane & (MB - 1);  // A fragment row (B^T row) within a block
+  const int fk = lane / MB;          // which 8-run of the MK-deep K step
+  // B transposed reads: the 16-lane group g covers columns +16*(g&1) and k rows +8*(g>>1) of a
+  // 32x16 step (32x32x16), or k rows +8*g of a 16x32 step (16x16x32); lane q of the group
+  // addresses row q/4, columns 4*(q%4).
   const int bg = lane >> 4, bq = lane & 15;
-  const int b_col_in = 16 * (bg & 1) + 4 * (bq & 3);  // column within the 32-block
-  const int b_k_in = 8 * (bg >> 1) + (bq >> 2);       // k row within the 16-step (first read)
+  const int b_col_in = (Cfg::MF16 ? 0 : 16 * (bg & 1)) + 4 * (bq & 3);  // column within the block
+  const int b_k_in = 8 * (Cfg::MF16 ? bg : (bg >> 1)) + (bq >> 2);      // k row within the step (first read)
 
   auto a_off = [&](int i, int ks) {
-    const int row = wm0 + 32 * i + frow;
-    const int chunk = ks * 2 + fk;
+    const int row = wm0 + MB * i + frow;
+    const int chunk = ks * (MK / 8) + fk;
     return row * (BK * 2) + ((chunk ^ swz_a<Cfg::A_ROW_CHUNKS>(row)) * 16);
   };
   auto b_off = [&](int j, int krow) {
-    const int col = wn0 + 32 * j + b_col_in;
+    const int col = wn0 + MB * j + b_col_in;
     return krow * (BN * 2) + (((col >> 3) ^ swz_b(krow)) * 16) + (col & 7) * 2;
   };
 
-  float16v acc[TM][TN];
+  using AccT = std::conditional_t<Cfg::MF16, float4v, float16v>;
+  AccT acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
+    for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
 
-  // Fragments of one whole K step (BK/16 substeps), double-buffered across steps: the MFMAs of
-  // step j run on set j&1 while the LDS reads of step j+1 fill set (j+1)&1.
-  constexpr int KS = BK / 16;
+  // Fragments of one whole K step (BK/MK MFMA substeps), double-buffered across steps: the MFMAs
+  // of step j run on set j&1 while the LDS reads of step j+1 fill set (j+1)&1.
+  constexpr int KS = BK / MK;
   half8 af[2][KS][TM], bf[2][KS][TN];
   // fragment read f of a step: f = ks * (TM + TN) + (i < TM ? i : TM + j)
   auto frag_op = [&](int buf, int st, int f) {
@@ -253,13 +271,13 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     } else if constexpr (PACKED_B) {
       // B^T stored [n][k] like A: one 16-byte read gives lane l the k-run of column l%32.
       const int j = w - TM;
-      const int row = wn0 + 32 * j + frow;
-      const int chunk = ks * 2 + fk;
+      const int row = wn0 + MB * j + frow;
+      const int chunk = ks * (MK / 8) + fk;
       bf[buf][ks][j] = *reinterpret_cast<const half8*>(
           &sB[st][row * (BK * 2) + ((chunk ^ swz_a<Cfg::A_ROW_CHUNKS>(row)) * 16)]);
     } else {
       const int j = w - TM;
-      const int krow = ks * 16 + b_k_in;
+      const int krow = ks * MK + b_k_in;
       const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(as_lds4(&sB[st][b_off(j, krow)]));
       const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(as_lds4(&sB[st][b_off(j, krow + 4)]));
       bf[buf][ks][j] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -272,7 +290,10 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // MFMA m of a step: m = (ks * TM + i) * TN + j
   auto mfma_op = [&](int buf, int m) {
     const int ks = m / (TM * TN), i = (m / TN) % TM, j = m % TN;
-    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
+    if constexpr (Cfg::MF16)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
+    else
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
   };
 
   static_assert(NSTAGE >= 3, "three stages at least");
@@ -420,30 +441,44 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   }
 
   // ---- epilogue: C = rscale[row] * acc + bias[col] ----
-  // Each wavefront moves its 32x32 accumulator blocks through a private 4 KB LDS scratch so that
-  // every lane ends up with 4 consecutive columns of one row: the result leaves in 16-byte (fp32)
-  // or 8-byte (fp16) stores, 4x fewer store instructions than one value per lane. The MFMA layout
-  // (lane l, register r -> column l%32, row 8*(r/4) + 4*(l/32) + r%4) puts rows R and R+4 in one
-  // write; storing row R at physical row R ^ ((R >> 2) & 1) gives them different bank halves.
+  // Each wavefront moves its accumulators, one 32x32 region at a time, through a private 4 KB LDS
+  // scratch so that every lane ends up with 4 consecutive columns of one row: the result leaves in
+  // 16-byte (fp32) or 8-byte (fp16) stores, 4x fewer store instructions than one value per lane.
+  //   32x32x16 layout (a region is one block): lane l, register r -> column l%32, row
+  //   8*(r/4) + 4*(l/32) + r%4. Rows R and R+4 meet in one write; storing row R at physical row
+  //   R ^ ((R >> 2) & 1) gives them different bank halves.
+  //   16x16x32 layout (a region is 2x2 blocks a, b): lane l, register r -> column 16b + l%16, row
+  //   16a + 4*(l/16) + r. One write covers rows 4g + r of the four 16-lane groups g; the same row
+  //   swizzle plus column ^ 16*((R >> 3) & 1) puts the four groups on four distinct 16-bank ranges.
+  // The read-back (two rows of 8 lanes per 16 lanes) hits both bank halves whole in either layout.
   __syncthreads();  // every wavefront's DMA has drained: the stages are free for scratch
   float* scr = reinterpret_cast<float*>(&sB[0][0] + wave * 4096);
   static_assert(Cfg::B_BYTES * NSTAGE >= 4096 * Cfg::WAVES, "scratch fits in the B stages");
+  auto phys = [](int row, int col) {
+    return (row ^ ((row >> 2) & 1)) * 32 + (Cfg::MF16 ? (col ^ (16 * ((row >> 3) & 1))) : col);
+  };
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+  for (int ri = 0; ri < Cfg::WTM / 32; ++ri) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+    for (int rj = 0; rj < Cfg::WTN / 32; ++rj) {
+      if constexpr (Cfg::MF16) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 8 * (r >> 2) + 4 * fk + (r & 3);
-        scr[(row ^ ((row >> 2) & 1)) * 32 + frow] = acc[i][j][r];
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) scr[phys(16 * a + 4 * fk + r, 16 * b + frow)] = acc[2 * ri + a][2 * rj + b][r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) scr[phys(8 * (r >> 2) + 4 * fk + (r & 3), frow)] = acc[ri][rj][r];
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int id = lane + 64 * q;
         const int row = id >> 3, c4 = (id & 7) * 4;
-        float4v v = *reinterpret_cast<const float4v*>(&scr[(row ^ ((row >> 2) & 1)) * 32 + c4]);
-        const int grow = m0 + wm0 + 32 * i + row;
-        const int gcol = n0 + wn0 + 32 * j + c4;
+        float4v v = *reinterpret_cast<const float4v*>(&scr[phys(row, c4)]);
+        const int grow = m0 + wm0 + 32 * ri + row;
+        const int gcol = n0 + wn0 + 32 * rj + c4;
         if (grow < M && gcol < N) {  // N % 8 == 0: a 4-column chunk is all in or all out
           const float rs = rscale != nullptr ? rscale[grow] : 1.f;
           const float4v b = bias != nullptr ? float4v{bias[gcol], bias[gcol + 1], bias[gcol + 2], bias[gcol + 3]}
