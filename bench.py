@@ -55,10 +55,11 @@ def parse(argv=None):
     ap.add_argument("--all", action="store_true",
                     help="also time every BASELINE configuration through the public API and write the per-config "
                          "table to --report (default gpurun_out/configs.json); the JSON line is unchanged")
-    ap.add_argument("--only", choices=["gemm", "rowscale", "skinny", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "rowscale", "skinny", "copy", "c1", "c3"], default=None,
                     help="launch just this kernel --steps times on the headline shapes (for rocprofv3 counter "
                          "runs) and print its average time; copy = a plain 256 MiB device copy, the "
-                         "calibration for FETCH_SIZE / WRITE_SIZE")
+                         "calibration for FETCH_SIZE / WRITE_SIZE; c1 / c3 = the C1 matmul 1024^3 and the "
+                         "C3 split-K 64x4096x1024 mm_t through the public API")
     ap.add_argument("--bert", action="store_true",
                     help="time only the BERT-base configuration (fp32 vs patch()) and print its JSON line")
     ap.add_argument("--peak", action="store_true",
@@ -479,6 +480,21 @@ def run_only(torch, lib, what: str, steps: int, dev) -> dict:
             lib.g16_skinny_f32in(x.data_ptr(), w.data_ptr(), out.data_ptr(), b.data_ptr(), M, N, K, ks,
                                  part.data_ptr(), part.numel(), cnt.data_ptr(), cnt.numel(), stream)
         bytes_moved = M * K * 4 + K * N * 2 + N * 4 + M * N * 4
+    elif what in ("c1", "c3"):
+        import gtx16_fp16 as g
+
+        if what == "c1":
+            M = K = N = 1024
+            a = randn((M, K), seed=0, dtype=torch.float16).to(dev)
+            w = randn((K, N), seed=1, dtype=torch.float16).to(dev)
+            fn = lambda: g.matmul(a, w)  # noqa: E731
+        else:
+            M, K, N = 64, 4096, 1024
+            a = randn((M, K), seed=0, dtype=torch.float16).to(dev)
+            w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(dev)
+            b = randn((N,), seed=2, scale=0.02).to(dev)
+            fn = lambda: g.mm_t(a, w, b)  # noqa: E731
+        bytes_moved = None
     else:
         M = K = N = 4096
         x = outlier_rows(randn((M, K), seed=0), 0.01, 2e3, 2e5, seed=3).to(dev)
@@ -503,7 +519,7 @@ def run_only(torch, lib, what: str, steps: int, dev) -> dict:
     if bytes_moved:
         res["GB/s"] = round(bytes_moved / (ms * 1e-3) / 1e9, 1)
     else:
-        res["TFLOP/s"] = round(2.0 * 4096 ** 3 / (ms * 1e-3) / 1e12, 1)
+        res["TFLOP/s"] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)
     return res
 
 
