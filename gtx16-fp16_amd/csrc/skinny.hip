@@ -150,8 +150,9 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
   if (!arrive_last_coherent(counters + strip * kCounterStride, static_cast<uint32_t>(ksplit))) return;
   if (c < N) {
     // Slices are added in slice order; loads are issued kZBatch slices at a time so their
-    // latencies overlap. Every slice, this one's included, is read back from the workspace.
-    constexpr int kZBatch = 8;
+    // latencies overlap (all 16 slices of the default plan in one round trip for M <= 2). Every
+    // slice, this one's included, is read back from the workspace.
+    constexpr int kZBatch = MM <= 2 ? 16 : 8;
     float s[MM];
 #pragma unroll
     for (int m = 0; m < MM; ++m) s[m] = 0.f;
