@@ -48,7 +48,8 @@ def parse(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     # ~30 ms of MFMA load brings the part to its working clock: with 5 warm-up steps the first timed
-    # steps still run slow (measured 869 vs 1001 TFLOPS for 5 vs 200 warm-up steps).
+    # steps still run slow (measured 869 vs 1001 TFLOPS for 5 vs 200 warm-up steps with the earlier
+    # 32x32x16 GEMM).
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--report", type=str, default=None, help="also write per-kernel details to this JSON file")
