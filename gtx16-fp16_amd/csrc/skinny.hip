@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
                                                           float* __restrict__ C, const float* __restrict__ bias,
                                                           float* __restrict__ part, uint32_t* __restrict__ counters,
                                                           int N, int K, int rows_per_wave, int ksplit, int nstrips) {
-  __shared__ float red[kWaves][kStripCols];
+  __shared__ float red[kWaves][MM][kStripCols];  // 16 KB per row of A
   const int strip = blockIdx.x % nstrips;
   const int kpart = blockIdx.x / nstrips;
   const int lane = threadIdx.x & (kWave - 1);
@@ -118,20 +118,23 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     }
   }
 
-  // Wavefronts -> thread t owns column strip*512 + t; sum the wavefronts in order.
+  // Wavefronts -> thread t owns column strip*512 + t; sum the wavefronts in order. Every row of A
+  // goes through LDS in the same round, so one barrier serves all of them.
   const int t = threadIdx.x;
   const int c = strip * kStripCols + t;
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    *reinterpret_cast<float4v*>(&red[wave][m][lane * 8]) = float4v{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+    *reinterpret_cast<float4v*>(&red[wave][m][lane * 8 + 4]) = float4v{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
+  }
+  __syncthreads();
   float mine[MM];
 #pragma unroll
   for (int m = 0; m < MM; ++m) {
-    *reinterpret_cast<float4v*>(&red[wave][lane * 8]) = float4v{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
-    *reinterpret_cast<float4v*>(&red[wave][lane * 8 + 4]) = float4v{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
-    __syncthreads();
-    float s = red[0][t];
+    float s = red[0][m][t];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) s += red[w][t];
+    for (int w = 1; w < kWaves; ++w) s += red[w][m][t];
     mine[m] = s;
-    __syncthreads();
   }
 
   if (ksplit == 1) {
