@@ -55,7 +55,7 @@ def parse(argv=None):
     ap.add_argument("--report", type=str, default=None, help="also write per-kernel details to this JSON file")
     ap.add_argument("--all", action="store_true",
                     help="also time every BASELINE configuration through the public API and write the per-config "
-                         "table to --report (default gpurun_out/configs.json); the JSON line is unchanged")
+                         "table to --report (default bench_configs.json in the working directory); the JSON line is unchanged")
     ap.add_argument("--only", choices=["gemm", "rowscale", "skinny", "copy", "c1", "c3"], default=None,
                     help="launch just this kernel --steps times on the headline shapes (for rocprofv3 counter "
                          "runs) and print its average time; copy = a plain 256 MiB device copy, the "
@@ -618,7 +618,7 @@ def main(argv=None) -> int:
         },
         "cpu_baseline": cpu,
     }
-    report = args.report or ("gpurun_out/configs.json" if args.all else None)
+    report = args.report or ("bench_configs.json" if args.all else None)
     if report:
         Path(report).parent.mkdir(parents=True, exist_ok=True)
         Path(report).write_text(json.dumps({"c4": c4, "skinny_m1": sk, "cpu": cpu, "configs": configs}, indent=2))
