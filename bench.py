@@ -288,8 +288,37 @@ def bench_all(torch, g, steps: int, dev) -> list:
 def bench_overhead(torch, g, dev, n: int = 1000) -> list:
     """Per-call host cost and wall time of FastLinear vs nn.Linear at one token (the decode path),
     as bench/overhead.py:9-29 of the reference measures it: `cpu` is the time to enqueue n calls,
-    `wall` the time until they have also finished on the GPU."""
+    `wall` the time until they have also finished on the GPU. `fast_linear_graph_us` is the same
+    FastLinear call replayed from a HIP graph of 32 captured calls (per call: replay time / 32),
+    which removes the host cost the reference's README (README.md:77) leaves to CUDA graphs."""
     import torch.nn as nn
+
+    def graph_cost(fl, x, calls: int = 32, reps: int = 50):
+        with torch.no_grad():
+            for _ in range(3):  # eager first: split buffers exist before capture (no fills recorded)
+                ref = fl(x)
+            torch.cuda.synchronize()
+            s = torch.cuda.Stream(dev)
+            s.wait_stream(torch.cuda.current_stream(dev))
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(s):
+                fl(x)
+                torch.cuda.synchronize()
+                with torch.cuda.graph(graph, stream=s):
+                    outs = [fl(x) for _ in range(calls)]
+            torch.cuda.current_stream(dev).wait_stream(s)
+            graph.replay()
+            torch.cuda.synchronize()
+            if not all(torch.equal(o, ref) for o in outs):
+                raise RuntimeError("graph replay differs from the eager FastLinear call")
+            for _ in range(5):
+                graph.replay()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            for _ in range(reps):
+                graph.replay()
+            torch.cuda.synchronize()
+            return round((time.perf_counter() - t) / (reps * calls) * 1e6, 2)
 
     def cost(fn):
         with torch.no_grad():
@@ -312,7 +341,8 @@ def bench_overhead(torch, g, dev, n: int = 1000) -> list:
         x = torch.randn(1, 1, K, device=dev)
         a, b = cost(lambda: lin(x)), cost(lambda: fl(x))
         rows.append({"config": f"decode overhead 1x{K}x{N}", "nn_linear_cpu_us": a[0], "nn_linear_wall_us": a[1],
-                     "fast_linear_cpu_us": b[0], "fast_linear_wall_us": b[1]})
+                     "fast_linear_cpu_us": b[0], "fast_linear_wall_us": b[1],
+                     "fast_linear_graph_us": graph_cost(fl, x)})
         print(json.dumps(rows[-1]), flush=True)
     return rows
 
