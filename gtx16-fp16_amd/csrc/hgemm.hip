@@ -356,33 +356,35 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     if (nk > 0) read_frags(0, 0);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __syncthreads();  // every wavefront holds step 0 in registers: stage 0 may be refilled
-    for (int it = 0; it < nk; it += 2) {
-      // two steps per trip so the fragment buffer index is a compile-time constant
+    // Step j on fragment buffer H (a compile-time constant, so two steps make one loop trip). The
+    // loop body has no branches: a conditional step or a conditional read inside it made the
+    // compiler copy accumulators between AGPRs and VGPRs on every trip (measured: ~3x slower
+    // steps). The last step's reads of step j+1 are harmless: they read a stage inside the ring
+    // (zeros or stale data) into the buffer no MFMA uses afterwards.
+    auto step = [&](auto hc, int j) {
+      constexpr int H = decltype(hc)::value;
+      const int kd = kbeg + (j + NSTAGE) * BK;
+      const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
+      const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b(kd);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int j = it + h;
-        if (j < nk) {
-          const int kd = kbeg + (j + NSTAGE) * BK;
-          const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
-          const bool next = j + 1 < nk;
-          const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b(kd);
+      for (int p = 0; p < PARTS; ++p) {
+        dma_op(std_, kd, ra, rb, p);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int p = 0; p < PARTS; ++p) {
-            dma_op(std_, kd, ra, rb, p);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(H, m);
 #pragma unroll
-            for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(h, m);
-            if (next) {
-#pragma unroll
-              for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(h ^ 1, stf, f);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          wait_dma_le<LAG * NDMA>();  // step j+2 has landed (this wavefront's part)
-          __syncthreads();            // ... every wavefront's part; step j+1 is in registers
-        }
+        for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      wait_dma_le<LAG * NDMA>();  // step j+2 has landed (this wavefront's part)
+      __syncthreads();            // ... every wavefront's part; step j+1 is in registers
+    };
+    int it = 0;
+    for (; it + 1 < nk; it += 2) {
+      step(std::integral_constant<int, 0>{}, it);
+      step(std::integral_constant<int, 1>{}, it + 1);
     }
+    if (it < nk) step(std::integral_constant<int, 0>{}, it);
   }
   wait_dma_le<0>();  // no DMA may still be writing LDS past this point
 
@@ -607,7 +609,7 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
 }  // namespace g16
 
 extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
-  // Split K when the output tiles cannot give every CU a workgroup, keeping >= 256 K per slice.
+  // Split K when the output tiles cannot give every CU a workgroup (slice sizes below).
   if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0) return 1;
   const g16::Plan p = g16::choose_tile(M, N, false);
   const int tiles = p.ntm * p.ntn;
@@ -617,9 +619,12 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   if (qtiles != tiles) return 1;
   // At most 8 slices: the last slice to arrive reads every other slice's fp32 tile at one CU's
   // bandwidth, so beyond ~8 the reduction costs more than the extra parallelism gains (measured:
-  // 64x4096x1024 12.9 us at 8 vs 14.7 us at 16; 64x1024x1024 and 512^3 best at their K/256 cap).
+  // 64x4096x1024 12.1 us at 8 vs 14.3 us at 16). Each slice keeps >= 256 K (>= 512 K for the
+  // 128x128 tile, whose 64 KB partials make the reduction dearer: 1024^3 14.2 us at 2 slices vs
+  // 15.3 us at 4, 512^3 10.0 us unsplit vs 10.8 us at 2; 64x1024x1024 on the 64x128 tile is best at
+  // its K/256 cap, 8.7 us at 4 vs 9.7 us at 2).
   int ks = g16::ceil_div(num_cus, tiles);
-  const int cap = K / 256;
+  const int cap = K / (q.tile == g16::Tile::T128 ? 512 : 256);
   ks = ks > cap ? cap : ks;
   ks = ks > 8 ? 8 : ks;
   return g16::ksplit_for(K, ks < 1 ? 1 : ks).ksplit;

@@ -123,6 +123,16 @@ def _check_operands(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | N
         raise ValueError(f"mm_t: bias must hold {N} values on x2d's device")
 
 
+def _cast_scratch(xbytes: int, M: int, dev: torch.device) -> tuple[torch.Tensor, int, int]:
+    # The fp16 copy of x (row-major or tile-packed, xbytes) and the M fp32 row scales share one
+    # allocation, 256-byte aligned parts: one caching-allocator call instead of two on a path whose
+    # per-call cost is host time at small shapes. Returns (owner, copy pointer, scales pointer).
+    off = (xbytes + 255) // 256 * 256
+    buf = torch.empty(off + 4 * M, device=dev, dtype=torch.uint8)
+    ptr = buf.data_ptr()
+    return buf, ptr, ptr + off
+
+
 def _aligned(x: torch.Tensor) -> torch.Tensor:
     # The kernels read activations as M*K contiguous values with 16-byte (rowscale) or dword
     # (skinny) loads from a 16-byte aligned base; supported() checks the weight's alignment only,
@@ -171,38 +181,32 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
 
     # GEMM path: fp16 inputs, with per-row power-of-two scaling for rows that would overflow.
     route = _gemm_route(lib, M, N, K, dev)
-    rscale = torch.empty(M, device=dev, dtype=torch.float32)
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
     f32in = x2d.dtype == torch.float32
     if route[0] == "packed":
         # Large GEMM: the cast writes the fp16 copy straight into the tile-packed layout the
         # 256x256 kernel streams (same values, same result).
-        xp = torch.empty(route[1] // 2, device=dev, dtype=torch.float16)
+        _scratch, xp, rscale = _cast_scratch(route[1], M, dev)
         rs_fn = lib.g16_rowscale_pack_f32 if f32in else lib.g16_rowscale_pack_f16
-        _clib.check(rs_fn(x2d.data_ptr(), xp.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
-                    "rowscale cast")
+        _clib.check(rs_fn(x2d.data_ptr(), xp, rscale, M, K, ROW_SCALE_THRESHOLD, stream), "rowscale cast")
         fn = lib.g16_hgemm_packed_f32out if out_dtype == torch.float32 else lib.g16_hgemm_packed_f16out
-        _clib.check(fn(xp.data_ptr(), w_t.data_ptr(), out.data_ptr(), bptr, rscale.data_ptr(), M, N, K, stream),
-                    "GEMM")
+        _clib.check(fn(xp, w_t.data_ptr(), out.data_ptr(), bptr, rscale, M, N, K, stream), "GEMM")
         return out
 
-    x16 = torch.empty(M, K, device=dev, dtype=torch.float16)
+    _scratch, x16, rscale = _cast_scratch(M * K * 2, M, dev)
     rs_fn = lib.g16_rowscale_f32 if f32in else lib.g16_rowscale_f16
-    _clib.check(rs_fn(x2d.data_ptr(), x16.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
-                "rowscale cast")
+    _clib.check(rs_fn(x2d.data_ptr(), x16, rscale, M, K, ROW_SCALE_THRESHOLD, stream), "rowscale cast")
 
     if route[0] == "splitk":
         # Too few output tiles to fill the GPU: split K, reduce the slices in a fixed order.
         _, ksplit, pbytes, cbytes = route
         bufs = split_buffers(dev, stream, pbytes, cbytes)
-        st = lib.g16_hgemm_splitk(x16.data_ptr(), w_t.data_ptr(), out.data_ptr(),
-                                  1 if out_dtype == torch.float16 else 0, bptr, rscale.data_ptr(),
-                                  M, N, K, ksplit, *bufs, stream)
+        st = lib.g16_hgemm_splitk(x16, w_t.data_ptr(), out.data_ptr(), 1 if out_dtype == torch.float16 else 0, bptr,
+                                  rscale, M, N, K, ksplit, *bufs, stream)
         _clib.check(st, "split-K GEMM")
         return out
     fn = lib.g16_hgemm_f32out if out_dtype == torch.float32 else lib.g16_hgemm_f16out
-    _clib.check(fn(x16.data_ptr(), w_t.data_ptr(), out.data_ptr(), bptr, rscale.data_ptr(), M, N, K, stream),
-                "GEMM")
+    _clib.check(fn(x16, w_t.data_ptr(), out.data_ptr(), bptr, rscale, M, N, K, stream), "GEMM")
     return out
 
 
@@ -247,15 +251,13 @@ def mm_t_prepacked(x2d: torch.Tensor, w_t: torch.Tensor, wp: torch.Tensor, bias:
     stream = stream_handle(dev.index or 0)
     b = None if bias is None else bias.float().contiguous()
     x2d = _aligned(x2d)
-    rscale = torch.empty(M, device=dev, dtype=torch.float32)
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
-    xp = torch.empty(lib.g16_packed_a_bytes(M, K) // 2, device=dev, dtype=torch.float16)
+    _scratch, xp, rscale = _cast_scratch(lib.g16_packed_a_bytes(M, K), M, dev)
     rs_fn = lib.g16_rowscale_pack_f32 if x2d.dtype == torch.float32 else lib.g16_rowscale_pack_f16
-    _clib.check(rs_fn(x2d.data_ptr(), xp.data_ptr(), rscale.data_ptr(), M, K, ROW_SCALE_THRESHOLD, stream),
-                "rowscale cast")
+    _clib.check(rs_fn(x2d.data_ptr(), xp, rscale, M, K, ROW_SCALE_THRESHOLD, stream), "rowscale cast")
     fn = lib.g16_hgemm_packed_ab_f32out if out_dtype == torch.float32 else lib.g16_hgemm_packed_ab_f16out
-    _clib.check(fn(xp.data_ptr(), wp.data_ptr(), out.data_ptr(), None if b is None else b.data_ptr(),
-                   rscale.data_ptr(), M, N, K, stream), "GEMM")
+    _clib.check(fn(xp, wp.data_ptr(), out.data_ptr(), None if b is None else b.data_ptr(), rscale, M, N, K, stream),
+                "GEMM")
     return out
 
 
