@@ -243,6 +243,35 @@ def test_splitk_fp16_output(lib, cuda):
     assert oracle.rel_err(_np(c.float()), ref) <= GEMM_TOL
 
 
+# (M, N, K step) picking the 128x128 (BK 32), 64x128 and 32x128 (BK 64) tiles
+SMALL_TILES = [(300, 264, 32), (64, 1024, 64), (20, 200, 64)]
+
+
+@pytest.mark.parametrize("M,N,bk", SMALL_TILES)
+@pytest.mark.parametrize("steps", [1, 2, 3, 5])
+def test_small_tiles_odd_and_even_step_counts(lib, cuda, M, N, bk, steps):
+    # The 4-wavefront tiles run their K loop in step pairs plus a tail step for an odd count: whole
+    # and ragged last steps, unsplit and in two slices (each slice has its own step count).
+    st = _stream(cuda)
+    for K in (bk * steps, bk * steps - 8):
+        a = randn((M, K), seed=steps, dtype=torch.float16).to(cuda)
+        b = randn((K, N), seed=steps + 1, scale=0.05, dtype=torch.float16).to(cuda)
+        bias = randn((N,), seed=2, scale=0.02).to(cuda)
+        s = torch.ones(M, device=cuda)
+        ref = oracle.gemm(_np(a), _np(s), _np(b), _np(bias), "float32")
+        c = torch.empty(M, N, device=cuda)
+        assert lib.g16_hgemm_f32out(a.data_ptr(), b.data_ptr(), c.data_ptr(), bias.data_ptr(), s.data_ptr(),
+                                    M, N, K, st) == 0
+        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2),
+                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2), cuda)
+        c2 = torch.empty(M, N, device=cuda)
+        assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c2.data_ptr(), 0, bias.data_ptr(), s.data_ptr(),
+                                    M, N, K, 2, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), st) == 0
+        torch.cuda.synchronize()
+        assert oracle.rel_err(_np(c), ref) <= GEMM_TOL, K
+        assert oracle.rel_err(_np(c2), ref) <= GEMM_TOL, K
+
+
 # ---------------------------------------------------------------------------------------------
 # skinny path (M <= 8)
 # ---------------------------------------------------------------------------------------------
