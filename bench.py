@@ -402,6 +402,46 @@ def bench_peak(torch, lib, dev) -> list:
     return rows
 
 
+def measured_peaks(torch, lib, dev) -> dict:
+    """The part's own ceilings for the two rooflines, next to the published peaks: the
+    register-only v_mfma_f32_16x16x32_f16 loop on random fp16 operands (bench.py --peak kind 5,
+    the rate a GEMM on real data can reach under the part's power limit, with the clock it held)
+    and the 4 GiB read stream at 16 workgroups per CU. Best of 3 launches after a warm-up each."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    clocks = torch.zeros(2, dtype=torch.int64, device=dev)
+    blocks, iters = cus * 2, 20000
+    out = torch.empty(blocks * 256, device=dev)
+    _clib_ok(lib.g16_peak_run(5, blocks, 100, out.data_ptr(), stream))
+    best, mhz = float("inf"), 0.0
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        _clib_ok(lib.g16_peak_run_clocked(5, blocks, iters, out.data_ptr(), clocks.data_ptr(), stream))
+        e1.record()
+        e1.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3
+        if t < best:
+            cyc, ticks = clocks.tolist()
+            best, mhz = t, (100.0 * cyc / ticks if ticks else 0.0)
+    mfma = lib.g16_peak_flops_per_lane_iter(5) * blocks * 256 * iters / best / 1e12
+    nbytes = 4 << 30
+    buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    sblocks = cus * 16
+    sout = torch.empty(sblocks * 256, device=dev)
+    _clib_ok(lib.g16_stream_read(buf.data_ptr(), nbytes, sblocks, sout.data_ptr(), stream))
+    sbest = float("inf")
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        _clib_ok(lib.g16_stream_read(buf.data_ptr(), nbytes, sblocks, sout.data_ptr(), stream))
+        e1.record()
+        e1.synchronize()
+        sbest = min(sbest, e0.elapsed_time(e1) * 1e-3)
+    del buf
+    return {"mfma_tflops": mfma, "mfma_clock_mhz": mhz, "stream_gbs": nbytes / sbest / 1e9}
+
+
 def _clib_ok(status: int) -> None:
     if status != 0:
         raise RuntimeError(f"peak kernel launch failed with status {status}")
@@ -596,6 +636,7 @@ def main(argv=None) -> int:
     c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev)
     sk = bench_skinny(torch, lib, g, args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch)
+    mp = measured_peaks(torch, lib, dev)
 
     gemm_tflops = c4["gemm_kernel_tflops"]
     line = {
@@ -623,6 +664,9 @@ def main(argv=None) -> int:
             "frac": round(gemm_tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "traffic": traffic_bytes("gemm"),
             "kernel_ms": round(c4["gemm_kernel_ms"], 5),
+            "measured_peak_random_operands": round(mp["mfma_tflops"], 1),
+            "measured_peak_clock_mhz": round(mp["mfma_clock_mhz"]),
+            "frac_of_measured_peak": round(gemm_tflops / mp["mfma_tflops"], 4),
         },
         "rowscale_kernel": {"kernel": "rowscale_kernel<float, packed> (g16_rowscale_pack_f32)", "ms": round(c4["rowscale_kernel_ms"], 5), "GB/s": round(c4["rowscale_kernel_gbs"], 1),
                             "frac_hbm": round(c4["rowscale_kernel_gbs"] / HBM_PEAK_GBS, 4),
@@ -641,6 +685,8 @@ def main(argv=None) -> int:
                 "frac": round(sk["kernel_gbs"] / HBM_PEAK_GBS, 4),
                 "traffic": traffic_bytes("skinny"),
                 "kernel_us": round(sk["kernel_us"], 3),
+                "measured_peak_read_stream": round(mp["stream_gbs"], 1),
+                "frac_of_measured_peak": round(sk["kernel_gbs"] / mp["stream_gbs"], 4),
             },
             "bytes_per_launch": sk["bytes_per_launch"],
             "ksplit": sk["ksplit"],
