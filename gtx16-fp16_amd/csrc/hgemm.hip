@@ -67,12 +67,19 @@ __device__ inline lds_short4v* as_lds4(const unsigned char* p) { return (lds_sho
 // inside the same statement; clang warns that m0 is reserved, but these kernels contain no other
 // reader of M0 (no LDS-direct, GWS or message instructions): in the generated assembly every
 // `s_mov_b32 m0` is one of these statements, immediately followed by its DMA.
-__device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, const unsigned char* lds, uint32_t off) {
-  const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds));
+// `lds_addr` is the LDS byte address (see lds_base) of the 1 KB the instruction fills.
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_addr, uint32_t off) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(off), "s"(rsrc)
                : "memory", "m0");
+}
+
+// LDS byte address of a __shared__ object, taken once per kernel: converting a generic pointer to
+// the LDS address space costs a 64-bit add and a null test, too much to repeat for every DMA
+// instruction of a loop that issues few other instructions.
+__device__ inline uint32_t lds_base(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)p));
 }
 
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int NSTAGE_, bool MF16_ = false>
@@ -143,6 +150,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   constexpr int BK = Cfg::BK, NSTAGE = Cfg::NSTAGE;
   __shared__ __attribute__((aligned(1024))) unsigned char sA[NSTAGE][Cfg::A_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char sB[NSTAGE][Cfg::B_BYTES];
+  const uint32_t sA_lds = lds_base(&sA[0][0]), sB_lds = lds_base(&sB[0][0]);
 
   // ---- tile assignment (XCD-aware, grouped) ----
   const int ntiles = ntm * ntn;
@@ -202,25 +210,25 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       // block; instruction q of the stage copies its q-th KB. ra is based at this tile row.
       const int q = wave * Cfg::A_INSTR + d;
       const uint32_t off = k0 < kend ? static_cast<uint32_t>(((k0 / BK) * 1024 + q * 64 + lane) * 16) : kOob;
-      dma16(ra, &sA[st][q * 1024], off);
+      dma16(ra, sA_lds + st * Cfg::A_BYTES + q * 1024, off);
     } else if (d < Cfg::A_INSTR) {
       const int row = a_row0 + d * Cfg::A_ROWS_PER_INSTR;
       const int c = a_phys ^ swz_a<Cfg::A_ROW_CHUNKS>(row);
       const bool ok = (m0 + row < M) && (k0 + c * 8 < kend);
       const uint32_t off = ok ? static_cast<uint32_t>((row * K + c * 8) * 2) : kOob;
-      dma16(ra, &sA[st][(wave * Cfg::A_INSTR + d) * 1024], off);
+      dma16(ra, sA_lds + st * Cfg::A_BYTES + (wave * Cfg::A_INSTR + d) * 1024, off);
     } else if (PACKED_B) {
       // Packed weight (g16_pack_weight): B^T's stage image, like packed A.
       const int q = wave * Cfg::B_INSTR + (d - Cfg::A_INSTR);
       const uint32_t off = k0 < kend ? static_cast<uint32_t>(((k0 / BK) * 1024 + q * 64 + lane) * 16) : kOob;
-      dma16(rb, &sB[st][q * 1024], off);
+      dma16(rb, sB_lds + st * Cfg::B_BYTES + q * 1024, off);
     } else {
       const int i = d - Cfg::A_INSTR;
       const int row = b_row0 + i * Cfg::B_ROWS_PER_INSTR;
       const int c = b_phys ^ swz_b(row);
       const bool ok = (k0 + row < kend) && (n0 + c * 8 < N);
       const uint32_t off = ok ? static_cast<uint32_t>((row * N + c * 8) * 2) : kOob;
-      dma16(rb, &sB[st][(wave * Cfg::B_INSTR + i) * 1024], off);
+      dma16(rb, sB_lds + st * Cfg::B_BYTES + (wave * Cfg::B_INSTR + i) * 1024, off);
     }
   };
   auto dma = [&](int st, int k0) {
