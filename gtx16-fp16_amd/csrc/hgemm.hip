@@ -55,8 +55,8 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) short4v lds_short4v;
 
-// Generic -> LDS address-space pointer (the transpose-read builtin takes one).
-__device__ inline lds_short4v* as_lds4(const unsigned char* p) { return (lds_short4v*)(p); }
+// LDS byte address -> LDS address-space pointer (the transpose-read builtin takes one).
+__device__ inline lds_short4v* lds4_at(uint32_t addr) { return reinterpret_cast<lds_short4v*>(static_cast<uintptr_t>(addr)); }
 
 // 16-byte DMA global -> LDS: lane i's chunk at buffer offset `off` lands at LDS byte lds + 16 i.
 // Issued as inline asm so the compiler's wait-counter bookkeeping does not see an LDS write it
@@ -209,8 +209,10 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       // Tile-packed A (g16_rowscale_pack_*): the stage image of step k0 is one contiguous 16 KB
       // block; instruction q of the stage copies its q-th KB. ra is based at this tile row.
       const int q = wave * Cfg::A_INSTR + d;
-      const uint32_t off = k0 < kend ? static_cast<uint32_t>(((k0 / BK) * 1024 + q * 64 + lane) * 16) : kOob;
-      dma16(ra, sA_lds + st * Cfg::A_BYTES + q * 1024, off);
+      // uniform part of the offset (kOob for a step past the slice) plus this lane's 16 bytes;
+      // the sum of kOob and a lane part (< 16 KB) is still past the descriptor's range: zeros
+      const uint32_t step_off = k0 < kend ? static_cast<uint32_t>(k0) / BK * 16384u : kOob;
+      dma16(ra, sA_lds + st * Cfg::A_BYTES + q * 1024, step_off + (q * 64 + lane) * 16);
     } else if (d < Cfg::A_INSTR) {
       const int row = a_row0 + d * Cfg::A_ROWS_PER_INSTR;
       const int c = a_phys ^ swz_a<Cfg::A_ROW_CHUNKS>(row);
@@ -220,8 +222,8 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     } else if (PACKED_B) {
       // Packed weight (g16_pack_weight): B^T's stage image, like packed A.
       const int q = wave * Cfg::B_INSTR + (d - Cfg::A_INSTR);
-      const uint32_t off = k0 < kend ? static_cast<uint32_t>(((k0 / BK) * 1024 + q * 64 + lane) * 16) : kOob;
-      dma16(rb, sB_lds + st * Cfg::B_BYTES + q * 1024, off);
+      const uint32_t step_off = k0 < kend ? static_cast<uint32_t>(k0) / BK * 16384u : kOob;
+      dma16(rb, sB_lds + st * Cfg::B_BYTES + q * 1024, step_off + (q * 64 + lane) * 16);
     } else {
       const int i = d - Cfg::A_INSTR;
       const int row = b_row0 + i * Cfg::B_ROWS_PER_INSTR;
@@ -235,6 +237,20 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
 #pragma unroll
     for (int d = 0; d < Cfg::DMA_PER_STEP; ++d) dma_op(st, k0, ra, rb, d);
+  };
+  // Inside the K loops, B's descriptor for successive steps comes from a running pointer (row-major
+  // B: one 64-bit add per step instead of a 64-bit multiply); b_run is set to the first step's base
+  // before each loop, and every call advances it by one step.
+  const _Float16* b_run = nullptr;
+  auto rsrc_b_next = [&](int k0) {
+    if constexpr (PACKED_B) {
+      return rsrc_b(k0);
+    } else {
+      const __amdgpu_buffer_rsrc_t r =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(b_run), 0, 0x7fffffff, kRawBufferDword3);
+      b_run += static_cast<size_t>(BK) * N;
+      return r;
+    }
   };
 
   // ---- fragment addressing (byte offsets within a stage) ----
@@ -259,6 +275,12 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     const int col = wn0 + MB * j + b_col_in;
     return krow * (BN * 2) + (((col >> 3) ^ swz_b(krow)) * 16) + (col & 7) * 2;
   };
+  // Every k row one lane reads in a step (b_k_in, +4, +MK per substep) has the same k % 4, hence
+  // the same swizzle: b_off(j, b_k_in + r) = b_off(j, b_k_in) + r * BN * 2. One LDS address per
+  // block, offset by the stage base, serves all of a step's transposing reads.
+  uint32_t b_tr[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) b_tr[j] = sB_lds + static_cast<uint32_t>(b_off(j, b_k_in));
 
   using AccT = std::conditional_t<Cfg::MF16, float4v, float16v>;
   AccT acc[TM][TN];
@@ -285,9 +307,9 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
           &sB[st][row * (BK * 2) + ((chunk ^ swz_a<Cfg::A_ROW_CHUNKS>(row)) * 16)]);
     } else {
       const int j = w - TM;
-      const int krow = ks * MK + b_k_in;
-      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(as_lds4(&sB[st][b_off(j, krow)]));
-      const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(as_lds4(&sB[st][b_off(j, krow + 4)]));
+      const uint32_t at = b_tr[j] + st * Cfg::B_BYTES + ks * MK * (BN * 2);
+      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds4_at(at));
+      const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds4_at(at + 4 * (BN * 2)));
       bf[buf][ks][j] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   };
@@ -324,6 +346,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       for (int s = 0; s < D; ++s) dma(s, kbeg + s * BK);
     }
     wait_dma_le<(D - 1) * NDMA>();  // step 0 has landed
+    b_run = B + static_cast<size_t>(kbeg + D * BK) * N + n0;
     phase_barrier();
     if (grp == 1) phase_barrier();
     for (int j = 0; j < nk; ++j) {
@@ -331,7 +354,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       read_frags(0, j % NSTAGE);
       {
         const int kd = kbeg + (j + D) * BK;
-        const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b(kd);
+        const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
 #pragma unroll
         for (int d = 0; d < NDMA; ++d) dma_op((j + D) % NSTAGE, kd, ra, rb, d);
       }
@@ -373,7 +396,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       constexpr int H = decltype(hc)::value;
       const int kd = kbeg + (j + NSTAGE) * BK;
       const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
-      const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b(kd);
+      const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
 #pragma unroll
       for (int p = 0; p < PARTS; ++p) {
         dma_op(std_, kd, ra, rb, p);
@@ -387,6 +410,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       wait_dma_le<LAG * NDMA>();  // step j+2 has landed (this wavefront's part)
       __syncthreads();            // ... every wavefront's part; step j+1 is in registers
     };
+    b_run = B + static_cast<size_t>(kbeg + NSTAGE * BK) * N + n0;
     int it = 0;
     for (; it + 1 < nk; it += 2) {
       step(std::integral_constant<int, 0>{}, it);
