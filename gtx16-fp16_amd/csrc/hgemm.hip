@@ -115,8 +115,8 @@ struct TileCfg {
 
 using Cfg256 = TileCfg<256, 256, 32, 2, 4, 4, true>;  // 8 wavefronts (two per SIMD), 4-stage ring, 128 KB
 using Cfg128 = TileCfg<128, 128, 32, 2, 2, 4>;  // 64 KB: two workgroups per CU
-using Cfg64 = TileCfg<64, 128, 64, 1, 4, 3>;
-using Cfg32 = TileCfg<32, 128, 64, 1, 4, 3>;
+using Cfg64 = TileCfg<64, 128, 64, 1, 4, 4>;
+using Cfg32 = TileCfg<32, 128, 64, 1, 4, 4>;
 
 // LDS swizzles (the LDS has 64 four-byte banks: a 256-byte period). A rows hold BK/8 chunks, so
 // 16/(BK/8) consecutive rows share one 256-byte bank period; XOR-ing the chunk with the index of
