@@ -350,7 +350,8 @@ def bench_overhead(torch, g, dev, n: int = 1000) -> list:
 def bench_peak(torch, lib, dev) -> list:
     """Instruction and HBM peaks of this part (the analogue of the reference's bench/peak.py):
     fp32 FMA, packed fp16 FMA and the two fp16 MFMA shapes from register-only loops (the MFMA ones
-    on near-constant and on random operand bits), and a streaming read of a 4 GiB buffer. Each is
+    on near-constant and on random operand bits), the LDS read bandwidth for 16-byte and
+    transposing reads, and a streaming read of a 4 GiB buffer. Each is
     the best of 3 timed launches after a warm-up; the instruction peaks also report the shader
     clock their loop ran at (s_memtime cycles over 100 MHz reference ticks)."""
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -380,6 +381,28 @@ def bench_peak(torch, lib, dev) -> list:
         rows.append({"peak": name, "TFLOP/s": round(flop / best / 1e12, 1), "ms": round(best * 1e3, 3),
                      "clock_MHz": round(mhz)})
         print(json.dumps(rows[-1]), flush=True)
+    for kind, name in ((6, "LDS read, ds_read_b128"), (7, "LDS transposing read, ds_read_b64_tr_b16")):
+        for per_cu in (1, 2, 4):  # 32 KB of LDS per workgroup: at most 5 per CU
+            blocks, iters = cus * per_cu, 20000
+            out = torch.empty(blocks * 256, device=dev)
+            _clib_ok(lib.g16_peak_run(kind, blocks, 100, out.data_ptr(), stream))
+            torch.cuda.synchronize()
+            best, mhz = float("inf"), 0.0
+            for _ in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                _clib_ok(lib.g16_peak_run_clocked(kind, blocks, iters, out.data_ptr(), clocks.data_ptr(), stream))
+                e1.record()
+                e1.synchronize()
+                t = e0.elapsed_time(e1) * 1e-3
+                if t < best:
+                    cyc, ticks = clocks.tolist()
+                    best, mhz = t, (100.0 * cyc / ticks if ticks else 0.0)
+            nb = lib.g16_peak_flops_per_lane_iter(kind) * blocks * 256 * iters
+            rows.append({"peak": f"{name} ({per_cu} workgroups/CU)", "GB/s": round(nb / best / 1e9, 1),
+                         "bytes_per_clk_per_CU": round(nb / best / (mhz * 1e6) / cus, 1) if mhz else None,
+                         "ms": round(best * 1e3, 3), "clock_MHz": round(mhz)})
+            print(json.dumps(rows[-1]), flush=True)
     nbytes = 4 << 30
     buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)
     for per_cu in (4, 8, 16):  # workgroups of 256 lanes per CU, 8 loads in flight per lane

@@ -111,21 +111,34 @@ struct TileCfg {
   static_assert(B_ROW_CHUNKS >= 16 && B_ROW_CHUNKS <= 64, "B swizzle needs >= 16 chunks per row");
   static constexpr int DMA_PER_STEP = A_INSTR + B_INSTR;  // per wavefront
   static_assert(NSTAGE >= 3 && (NSTAGE - 2) * DMA_PER_STEP <= 63, "vmcnt range");
+  static_assert(!MF16 || A_ROW_CHUNKS == 4, "the 16x16x32 tile's A stage is the packed image");
+
+  // LDS chunk swizzles (the LDS has 64 four-byte banks: a 256-byte period). Which lanes one LDS
+  // cycle serves is not a plain run of consecutive lanes, so the forms below were chosen by
+  // measuring read patterns on the part (cycles per read instruction with the LDS saturated):
+  //   A (and the packed B^T): row r keeps chunk c at c ^ swz_a(r). 32x32 fragments (lane l: row
+  //   l % 32, chunk l / 32): (r / (16 / RC)) % RC. 16x16x32 fragments (lane l: row l % 16, chunk
+  //   l / 16): (r / 2) % 4, the packed layout's swizzle; (r / 4) % 4 doubled their read time.
+  //   B (row-major, transposing reads; a 32-lane half reads 16 columns of 8 k rows): row k keeps
+  //   chunk c at c ^ swz_b(k). With 128 columns (32x32 blocks), 4 * (k % 4); with 256 columns and
+  //   16x16x32 blocks (k rows 0-3 and 8-11 in one half), 2 * (k % 4 + 4 * ((k / 8) % 2)), which
+  //   puts the 8 rows' 32-byte pieces on 8 distinct bank ranges (4 * (k % 4) paired rows k and
+  //   k + 8: 1.7x the read time). Both forms give every k row a lane reads in one step (k, k + 4,
+  //   and k + MK on later substeps) the same swizzle.
+  __device__ static int swz_a(int row) {
+    if constexpr (MF16) return pack_swz(row);
+    else return (row / (16 / A_ROW_CHUNKS)) % A_ROW_CHUNKS;
+  }
+  __device__ static int swz_b(int k) {
+    if constexpr (MF16) return ((k & 3) + 4 * ((k >> 3) & 1)) << 1;
+    else return (k & 3) << 2;
+  }
 };
 
 using Cfg256 = TileCfg<256, 256, 32, 2, 4, 4, true>;  // 8 wavefronts (two per SIMD), 4-stage ring, 128 KB
 using Cfg128 = TileCfg<128, 128, 32, 2, 2, 4>;  // 64 KB: two workgroups per CU
 using Cfg64 = TileCfg<64, 128, 64, 1, 4, 4>;
 using Cfg32 = TileCfg<32, 128, 64, 1, 4, 4>;
-
-// LDS swizzles (the LDS has 64 four-byte banks: a 256-byte period). A rows hold BK/8 chunks, so
-// 16/(BK/8) consecutive rows share one 256-byte bank period; XOR-ing the chunk with the index of
-// that row group keeps 16 consecutive rows of one chunk column on distinct banks (the 16 lanes of a
-// 16-byte read). B: the transposing reads of a 32-lane half touch 4 consecutive rows x 4 chunks,
-// which XOR with 4*(k%4) spreads over 16 distinct chunk positions.
-template <int RC>
-__device__ inline int swz_a(int row) { return (row / (16 / RC)) % RC; }
-__device__ inline int swz_b(int k) { return (k & 3) << 2; }
 
 // s_waitcnt vmcnt(N) with expcnt/lgkmcnt left alone: waits until at most N of this wavefront's
 // vector-memory operations (here: the DMA of younger stages) are still in flight.
@@ -215,7 +228,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       dma16(ra, sA_lds + st * Cfg::A_BYTES + q * 1024, step_off + (q * 64 + lane) * 16);
     } else if (d < Cfg::A_INSTR) {
       const int row = a_row0 + d * Cfg::A_ROWS_PER_INSTR;
-      const int c = a_phys ^ swz_a<Cfg::A_ROW_CHUNKS>(row);
+      const int c = a_phys ^ Cfg::swz_a(row);
       const bool ok = (m0 + row < M) && (k0 + c * 8 < kend);
       const uint32_t off = ok ? static_cast<uint32_t>((row * K + c * 8) * 2) : kOob;
       dma16(ra, sA_lds + st * Cfg::A_BYTES + (wave * Cfg::A_INSTR + d) * 1024, off);
@@ -227,7 +240,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     } else {
       const int i = d - Cfg::A_INSTR;
       const int row = b_row0 + i * Cfg::B_ROWS_PER_INSTR;
-      const int c = b_phys ^ swz_b(row);
+      const int c = b_phys ^ Cfg::swz_b(row);
       const bool ok = (k0 + row < kend) && (n0 + c * 8 < N);
       const uint32_t off = ok ? static_cast<uint32_t>((row * N + c * 8) * 2) : kOob;
       dma16(rb, sB_lds + st * Cfg::B_BYTES + (wave * Cfg::B_INSTR + i) * 1024, off);
@@ -269,15 +282,15 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   auto a_off = [&](int i, int ks) {
     const int row = wm0 + MB * i + frow;
     const int chunk = ks * (MK / 8) + fk;
-    return row * (BK * 2) + ((chunk ^ swz_a<Cfg::A_ROW_CHUNKS>(row)) * 16);
+    return row * (BK * 2) + ((chunk ^ Cfg::swz_a(row)) * 16);
   };
   auto b_off = [&](int j, int krow) {
     const int col = wn0 + MB * j + b_col_in;
-    return krow * (BN * 2) + (((col >> 3) ^ swz_b(krow)) * 16) + (col & 7) * 2;
+    return krow * (BN * 2) + (((col >> 3) ^ Cfg::swz_b(krow)) * 16) + (col & 7) * 2;
   };
-  // Every k row one lane reads in a step (b_k_in, +4, +MK per substep) has the same k % 4, hence
-  // the same swizzle: b_off(j, b_k_in + r) = b_off(j, b_k_in) + r * BN * 2. One LDS address per
-  // block, offset by the stage base, serves all of a step's transposing reads.
+  // Every k row one lane reads in a step (b_k_in, +4, +MK per substep) has the same swizzle (see
+  // swz_b): b_off(j, b_k_in + r) = b_off(j, b_k_in) + r * BN * 2. One LDS address per block, offset
+  // by the stage base, serves all of a step's transposing reads.
   uint32_t b_tr[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) b_tr[j] = sB_lds + static_cast<uint32_t>(b_off(j, b_k_in));
@@ -304,7 +317,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       const int row = wn0 + MB * j + frow;
       const int chunk = ks * (MK / 8) + fk;
       bf[buf][ks][j] = *reinterpret_cast<const half8*>(
-          &sB[st][row * (BK * 2) + ((chunk ^ swz_a<Cfg::A_ROW_CHUNKS>(row)) * 16)]);
+          &sB[st][row * (BK * 2) + ((chunk ^ Cfg::swz_a(row)) * 16)]);
     } else {
       const int j = w - TM;
       const uint32_t at = b_tr[j] + st * Cfg::B_BYTES + ks * MK * (BN * 2);

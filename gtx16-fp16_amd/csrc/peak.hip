@@ -10,6 +10,10 @@
 //           ones of kinds 2, 3. The MFMA datapath's power depends on how many operand bits toggle,
 //           and the part lowers its clock to hold its power limit, so these give the rate a GEMM
 //           on real data can reach; 2 and 3 give the rate at the part's top clock.
+//   kind 6: LDS reads, ds_read_b128 (16 bytes per lane), 8 in flight per wavefront;
+//   kind 7: LDS transposing reads, ds_read_b64_tr_b16 (8 bytes per lane), 8 in flight;
+//           kinds 6 and 7 give the LDS read bandwidth a CU sustains for the two fragment reads
+//           the GEMM issues (A fragments are 16-byte reads, B fragments transposing reads);
 // and a streaming read of a large buffer (16-byte loads, grid-stride) for HBM bandwidth.
 // Everything stays in registers except the read stream; results are folded into `out` so the
 // compiler cannot drop the work. Workgroup 0's first wavefront can also report the shader clock
@@ -136,6 +140,53 @@ __global__ __launch_bounds__(256) void peak_mfma16(float* out, unsigned long lon
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// LDS read bandwidth: every wavefront reads 8 contiguous pieces of 64 lanes x W bytes (W = 16 for
+// ds_read_b128, 8 for ds_read_b64_tr_b16; contiguous lanes touch distinct banks) from a 32 KB
+// buffer, then waits for them; the reads are inline asm (volatile, with a memory clobber) so the
+// compiler can neither drop, hoist nor merge them. Offsets stay inside the buffer: lane base
+// < 256 * 16 = 4 KB and piece offsets d * 4 KB (d < 8), so the last byte read is below 32 KB.
+// 32 KB per workgroup lets five workgroups (20 wavefronts) share a CU's 160 KB.
+#define G16_LDS_READ8(INSN, V, A)                                                                  \
+  asm volatile(INSN " %0, %8 offset:0\n\t" INSN " %1, %8 offset:4096\n\t" INSN " %2, %8 offset:8192\n\t" \
+               INSN " %3, %8 offset:12288\n\t" INSN " %4, %8 offset:16384\n\t" INSN " %5, %8 offset:20480\n\t" \
+               INSN " %6, %8 offset:24576\n\t" INSN " %7, %8 offset:28672\n\ts_waitcnt lgkmcnt(0)"    \
+               : "=v"(V[0]), "=v"(V[1]), "=v"(V[2]), "=v"(V[3]), "=v"(V[4]), "=v"(V[5]), "=v"(V[6]),     \
+                 "=v"(V[7])                                                                           \
+               : "v"(A)                                                                               \
+               : "memory")
+
+template <bool TR>
+__global__ __launch_bounds__(256) void peak_lds(float* out, unsigned long long* clk, float seed, int iters) {
+  __shared__ u32x4 buf[2048];  // 32 KB
+  for (int i = threadIdx.x; i < 2048; i += 256) {
+    const uint32_t u = static_cast<uint32_t>(i) + static_cast<uint32_t>(seed);
+    buf[i] = u32x4{u, u ^ 0x5555u, u * 3u, u * 7u};
+  }
+  __syncthreads();
+  const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                            (__attribute__((address_space(3))) void*)&buf[0])) +
+                        threadIdx.x * (TR ? 8u : 16u);
+  uint32_t acc = 0;
+  LoopClock lc;
+  lc.start();
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (TR) {
+      u32x2 v[8];
+      G16_LDS_READ8("ds_read_b64_tr_b16", v, base);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc ^= v[d].x;
+    } else {
+      u32x4 v[8];
+      G16_LDS_READ8("ds_read_b128", v, base);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc ^= v[d].x;
+    }
+  }
+  lc.stop(clk);
+  out[blockIdx.x * blockDim.x + threadIdx.x] = static_cast<float>(acc & 0xffu);
+}
+#undef G16_LDS_READ8
+
 // Grid-stride read of n16 16-byte chunks; every lane folds what it read into one float.
 __global__ __launch_bounds__(256) void stream_read(const u32x4* __restrict__ p, size_t n16, float* out) {
   uint32_t acc = 0;
@@ -160,12 +211,15 @@ __global__ __launch_bounds__(256) void stream_read(const u32x4* __restrict__ p, 
 }  // namespace g16
 
 extern "C" double g16_peak_flops_per_lane_iter(int kind) {
-  // flops one lane contributes per loop iteration (MFMA: a wavefront's flops / 64)
+  // work one lane contributes per loop iteration: flops for kinds 0-5 (MFMA: a wavefront's
+  // flops / 64), LDS bytes read for kinds 6 and 7
   switch (kind) {
     case 0: return 8.0 * 2;                          // 8 fp32 FMAs
     case 1: return 8.0 * 2 * 2;                      // 8 packed fp16 FMAs
     case 2: case 4: return 8.0 * 32 * 32 * 16 * 2 / 64;      // 8 MFMA 32x32x16
     case 3: case 5: return 16.0 * 16 * 16 * 32 * 2 / 64;     // 16 MFMA 16x16x32
+    case 6: return 8.0 * 16;                         // LDS bytes: 8 ds_read_b128
+    case 7: return 8.0 * 8;                          // LDS bytes: 8 ds_read_b64_tr_b16
     default: return 0.0;
   }
 }
@@ -184,6 +238,8 @@ extern "C" int g16_peak_run_clocked(int kind, int blocks, int iters, float* out,
     case 3: return g16::launch(g16::peak_mfma16<false>, grid, block, s, out, clocks, 1e-3f, iters);
     case 4: return g16::launch(g16::peak_mfma32<true>, grid, block, s, out, clocks, 1e-3f, iters);
     case 5: return g16::launch(g16::peak_mfma16<true>, grid, block, s, out, clocks, 1e-3f, iters);
+    case 6: return g16::launch(g16::peak_lds<false>, grid, block, s, out, clocks, 1.0f, iters);
+    case 7: return g16::launch(g16::peak_lds<true>, grid, block, s, out, clocks, 1.0f, iters);
     default: return G16_E_DTYPE;
   }
 }

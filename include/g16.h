@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 6
+#define G16_ABI_VERSION 7
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -88,7 +88,7 @@ int g16_hgemm_f16out(const uint16_t* A, const uint16_t* B, uint16_t* C, const fl
  * of row-major. Same values, same results bit for bit; only the intermediate's layout differs.
  *   Packed layout of Yp: blocks of 256 rows x 32 columns, block (tm, ks) at block index
  *   tm * ceil(K/32) + ks, 16 KB each; inside a block, 16-byte chunk q*64 + i (q < 16, i < 64)
- *   holds columns 8*((i % 4) ^ ((r / 4) % 4)) .. +7 of local row r = 16q + i/4. Rows >= M and
+ *   holds columns 8*((i % 4) ^ ((r / 2) % 4)) .. +7 of local row r = 16q + i/4. Rows >= M and
  *   columns >= K are written as zeros. g16_packed_a_bytes() gives the size.
  * g16_hgemm_use_packed() is 1 where mm_t takes this route (the plain plan would use the 256x256
  * tile without a split), else 0. The packed GEMM accepts any shape.
@@ -162,9 +162,12 @@ int g16_skinny_plan(int M, int N, int K, int num_cus);
  * and bandwidth peaks the benchmark's rooflines divide by, at the clocks the part holds.
  * kind 0: fp32 FMA (VALU); 1: packed fp16 FMA; 2: MFMA 32x32x16 f16; 3: MFMA 16x16x32 f16;
  * 4, 5: kinds 2, 3 on random fp16 operand bits (the MFMA power, hence the clock the part holds,
- * depends on operand toggling: 2 and 3 run at the top clock, 4 and 5 at the clock real data gets).
+ * depends on operand toggling: 2 and 3 run at the top clock, 4 and 5 at the clock real data gets);
+ * 6: LDS reads with ds_read_b128; 7: LDS transposing reads with ds_read_b64_tr_b16 (32 KB of LDS
+ * per workgroup, so at most five workgroups share a CU).
  * g16_peak_run launches `blocks` workgroups of 256 lanes looping `iters` times; each lane does
- * g16_peak_flops_per_lane_iter(kind) flops per iteration. `out` holds blocks * 256 floats.
+ * g16_peak_flops_per_lane_iter(kind) flops (kinds 0-5) or LDS bytes (kinds 6, 7) per iteration.
+ * `out` holds blocks * 256 floats.
  * g16_peak_run_clocked does the same and, when `clocks` is not NULL, stores into clocks[0] the
  * shader clock cycles and into clocks[1] the 100 MHz reference ticks of workgroup 0's loop.
  * g16_stream_read reads `bytes` (a multiple of 16, 16-byte aligned buffer) once with 16-byte

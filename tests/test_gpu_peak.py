@@ -16,7 +16,7 @@ def lib(cuda):
     return _clib.load()
 
 
-@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4, 5, 6, 7])
 def test_peak_kernels_run(lib, cuda, kind):
     blocks = 8
     out = torch.full((blocks * 256,), float("nan"), device=cuda)
@@ -27,7 +27,7 @@ def test_peak_kernels_run(lib, cuda, kind):
     assert lib.g16_peak_flops_per_lane_iter(kind) > 0
 
 
-@pytest.mark.parametrize("kind", [0, 4])
+@pytest.mark.parametrize("kind", [0, 4, 6])
 def test_peak_clock_readout(lib, cuda, kind):
     # workgroup 0's loop: shader cycles and 100 MHz reference ticks give a clock in the part's range
     blocks, iters = 8, 20000
@@ -57,6 +57,24 @@ def test_peak_fp32_fma_value(lib, cuda):
     for i in range(8):
         s = (s + x[:, i]).astype(np.float32)
     assert np.array_equal(out.cpu().numpy(), s)
+
+
+@pytest.mark.parametrize("iters", [1, 3])
+def test_peak_lds_read_value(lib, cuda, iters):
+    # kind 6: word 4i of the 32 KB buffer holds i + 1; lane t reads 16-byte elements
+    # t + 256 d (d < 8) every iteration and XORs their first words
+    blocks = 2
+    out = torch.empty(blocks * 256, device=cuda)
+    st = torch.cuda.current_stream(cuda).cuda_stream
+    assert lib.g16_peak_run(6, blocks, iters, out.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    t = np.arange(256, dtype=np.uint32)
+    acc = np.zeros(256, dtype=np.uint32)
+    for it in range(iters):
+        for d in range(8):
+            acc ^= t + 256 * d + 1
+    want = np.tile((acc & 0xFF).astype(np.float32), blocks)
+    assert np.array_equal(out.cpu().numpy(), want)
 
 
 def test_stream_read_and_rejects(lib, cuda):

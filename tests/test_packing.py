@@ -23,7 +23,7 @@ def test_pack_a_places_every_element_and_zero_pads(M, K):
 
 def test_pack_a_block_is_the_stage_image():
     # Block (0, 0), chunk q*64 + i holds local row 16q + i//4; its four chunks permute the four
-    # 8-column groups of that row by XOR with (row // 4) % 4.
+    # 8-column groups of that row by XOR with (row // 2) % 4.
     y = np.zeros((256, 32), dtype=np.float16)
     for r in range(256):
         for c in range(4):
@@ -32,7 +32,7 @@ def test_pack_a_block_is_the_stage_image():
     for q in range(16):
         for i in range(64):
             r = 16 * q + i // 4
-            c = (i % 4) ^ ((r // 4) % 4)
+            c = (i % 4) ^ ((r // 2) % 4)
             assert (p[q * 64 + i] == r * 4 + c).all()
 
 
