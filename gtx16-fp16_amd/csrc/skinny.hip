@@ -247,17 +247,32 @@ int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, i
 }  // namespace g16
 
 extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
-  // One 8-wavefront workgroup per two CUs (measured faster than one per CU for M = 1..8: fewer,
-  // longer K slices make the split reduction shorter), each wavefront streaming >= kMinRows rows.
+  // One 8-wavefront workgroup per CU for M <= 2 and per two CUs for larger M, each wavefront
+  // streaming >= kMinRows rows. Measured over split factors 4-64 (graph-timed, weights rotated
+  // past the Infinity Cache): one per CU is 3-22 % faster at M = 1, 2 for K x N = 4096^2,
+  // 11008 x 4096 and 8192^2 (1 x 8192^2: 30.5 -> 23.7 us); at M = 4 the extra slices cost more
+  // in the split reduction (4096^2: 13.3 vs 16.2 us).
   if (N <= 0 || K <= 0 || num_cus <= 0) return 1;
   const int nstrips = g16::ceil_div(N, g16::kStripCols);
-  const int target = (num_cus + 1) / 2;
-  int ks = g16::ceil_div(target, nstrips);
+  // M <= 2 rounds down so that the grid never exceeds one workgroup per CU: a few workgroups past
+  // that run as a second round after the first (1 x 4096 x 14336 at 280 workgroups: 28.9 us;
+  // at 224: 21.9 us).
+  int ks = M <= 2 ? num_cus / nstrips : g16::ceil_div((num_cus + 1) / 2, nstrips);
   // M = 1 keeps a full 16-row block per wavefront (6.3 vs 7.2 us at 1x1024x3072); larger M gain
   // more from the extra slices than they lose to a partial block (10.8 vs 11.3 us at 4x1024x3072).
   const int min_rows = M == 1 ? 16 : g16::kMinRows;
   const int cap = K / (g16::kWaves * min_rows) > 1 ? K / (g16::kWaves * min_rows) : 1;
   ks = ks < 1 ? 1 : (ks > cap ? cap : ks);
+  if (M <= 2) {
+    // Prefer a split that gives every wavefront whole blocks of rows_in_flight() = 16 rows, if one
+    // is within a factor of two (1 x 4096 x 12288: 8 slices 18.5 us, 10 slices 19.8 us).
+    for (int d = ks; d > ks / 2; --d) {
+      if (K % (g16::kWaves * 16 * d) == 0) {
+        ks = d;
+        break;
+      }
+    }
+  }
   return g16::split_for(K, ks).ksplit;
 }
 
