@@ -20,6 +20,8 @@
 //     device-coherent stores and the last slice to arrive (per strip) adds the slices in slice
 //     order. No floating-point atomics: results are bitwise reproducible and C needs no zero-fill
 //     (the reference zero-fills C and accumulates with atomicAdd, kernels.py:205-206).
+#include <type_traits>
+
 #include "g16_common.hpp"
 
 namespace g16 {
@@ -118,64 +120,100 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     }
   }
 
-  // Wavefronts -> thread t owns column strip*512 + t; sum the wavefronts in order. Every row of A
-  // goes through LDS in the same round, so one barrier serves all of them.
-  const int t = threadIdx.x;
-  const int c = strip * kStripCols + t;
+  // Wavefronts -> LDS, then the strip's MM x 512 sums are handed out in groups of kGW consecutive
+  // columns of one row (4 for M >= 4, so that the split reduction moves them with 16-byte coherent
+  // accesses; single columns below that, which keeps all 512 threads busy): group g is row
+  // g / (512 / kGW), columns strip*512 + kGW*(g % (512 / kGW)) .., summed over the wavefronts in
+  // order. Every row of A goes through LDS in the same round, so one barrier serves all of them.
 #pragma unroll
   for (int m = 0; m < MM; ++m) {
     *reinterpret_cast<float4v*>(&red[wave][m][lane * 8]) = float4v{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
     *reinterpret_cast<float4v*>(&red[wave][m][lane * 8 + 4]) = float4v{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
   }
   __syncthreads();
-  float mine[MM];
+  constexpr int kGW = MM >= 4 ? 4 : 1;
+  using V = std::conditional_t<kGW == 4, float4v, float>;
+  constexpr int kRowGroups = kStripCols / kGW;
+  constexpr int kGroups = MM * kRowGroups;
+  constexpr int kGroupsPerThread = (kGroups + kThreads - 1) / kThreads;
+  const int t = threadIdx.x;
+  // M = 5..7: the last round of groups covers only part of the threads
+  auto group_in = [&](int i) { return kGroups % kThreads == 0 || t + i * kThreads < kGroups; };
+  auto group_row = [&](int i) { return (t + i * kThreads) / kRowGroups; };
+  auto group_col = [&](int i) { return strip * kStripCols + ((t + i * kThreads) % kRowGroups) * kGW; };
+  auto group_live = [&](int i) { return group_in(i) && group_col(i) < N; };  // N % 8 == 0: whole groups
+  auto lds_at = [&](int w, int i) {
+    const float* p = &red[w][group_row(i)][group_col(i) - strip * kStripCols];
+    if constexpr (kGW == 4) return *reinterpret_cast<const float4v*>(p);
+    else return *p;
+  };
+  V mine[kGroupsPerThread];
 #pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    float s = red[0][m][t];
+  for (int i = 0; i < kGroupsPerThread; ++i) {
+    mine[i] = V{};
+    if (group_in(i)) {
+      V s = lds_at(0, i);
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) s += red[w][m][t];
-    mine[m] = s;
+      for (int w = 1; w < kWaves; ++w) s += lds_at(w, i);
+      mine[i] = s;
+    }
   }
+  auto store_out = [&](int i, V v) {
+    const int c = group_col(i);
+    float* o = C + static_cast<size_t>(group_row(i)) * N + c;
+    if constexpr (kGW == 4) {
+      if (bias != nullptr) v += float4v{bias[c], bias[c + 1], bias[c + 2], bias[c + 3]};
+      *reinterpret_cast<float4v*>(o) = v;
+    } else {
+      *o = v + (bias != nullptr ? bias[c] : 0.f);
+    }
+  };
 
   if (ksplit == 1) {
-    if (c < N) {
-      const float b = bias ? bias[c] : 0.f;
 #pragma unroll
-      for (int m = 0; m < MM; ++m) C[static_cast<size_t>(m) * N + c] = mine[m] + b;
-    }
+    for (int i = 0; i < kGroupsPerThread; ++i)
+      if (group_live(i)) store_out(i, mine[i]);
     return;
   }
 
-  if (c < N) {
+  // slice z's partial of group i sits at float offset (z * MM + row) * N + col of the workspace
+  const __amdgpu_buffer_rsrc_t slices = coherent_rsrc(part, static_cast<uint32_t>(ksplit) * MM * N * 4u);
+  auto slot = [&](int z, int i) { return (static_cast<size_t>(z) * MM + group_row(i)) * N + group_col(i); };
+  auto publish = [&](int i, V v) {
+    if constexpr (kGW == 4) store_coherent4(slices, static_cast<uint32_t>(slot(kpart, i) * 4u), v);
+    else store_coherent(part + slot(kpart, i), v);
+  };
+  auto fetch = [&](int z, int i) -> V {
+    if constexpr (kGW == 4) return load_coherent4(slices, static_cast<uint32_t>(slot(z, i) * 4u));
+    else return load_coherent(part + slot(z, i));
+  };
 #pragma unroll
-    for (int m = 0; m < MM; ++m) store_coherent(part + (static_cast<size_t>(kpart) * MM + m) * N + c, mine[m]);
-  }
+  for (int i = 0; i < kGroupsPerThread; ++i)
+    if (group_live(i)) publish(i, mine[i]);
   if (!arrive_last_coherent(counters + strip * kCounterStride, static_cast<uint32_t>(ksplit))) return;
-  if (c < N) {
-    // Slices are added in slice order; loads are issued kZBatch slices at a time so their
-    // latencies overlap (all 16 slices of the default plan in one round trip for M <= 2). Every
-    // slice, this one's included, is read back from the workspace.
-    constexpr int kZBatch = MM <= 2 ? 16 : 8;
-    float s[MM];
+  // Slices are added in slice order; loads are issued kZBatch slices at a time (for all of the
+  // thread's groups) so their latencies overlap. Every slice, this one's included, is read back
+  // from the workspace.
+  constexpr int kZBatch = MM <= 2 ? 16 : 8;
+  V s[kGroupsPerThread];
 #pragma unroll
-    for (int m = 0; m < MM; ++m) s[m] = 0.f;
-    for (int z0 = 0; z0 < ksplit; z0 += kZBatch) {
-      float v[kZBatch][MM];
+  for (int i = 0; i < kGroupsPerThread; ++i) s[i] = V{};
+  for (int z0 = 0; z0 < ksplit; z0 += kZBatch) {
+    V v[kZBatch][kGroupsPerThread];
 #pragma unroll
-      for (int b = 0; b < kZBatch; ++b)
+    for (int b = 0; b < kZBatch; ++b)
 #pragma unroll
-        for (int m = 0; m < MM; ++m)
-          v[b][m] = z0 + b < ksplit ? load_coherent(part + (static_cast<size_t>(z0 + b) * MM + m) * N + c) : 0.f;
+      for (int i = 0; i < kGroupsPerThread; ++i)
+        v[b][i] = (z0 + b < ksplit && group_live(i)) ? fetch(z0 + b, i) : V{};
 #pragma unroll
-      for (int b = 0; b < kZBatch; ++b)
+    for (int b = 0; b < kZBatch; ++b)
 #pragma unroll
-        for (int m = 0; m < MM; ++m)
-          if (z0 + b < ksplit) s[m] += v[b][m];
-    }
-    const float bb = bias ? bias[c] : 0.f;
-#pragma unroll
-    for (int m = 0; m < MM; ++m) C[static_cast<size_t>(m) * N + c] = s[m] + bb;
+      for (int i = 0; i < kGroupsPerThread; ++i)
+        if (z0 + b < ksplit) s[i] += v[b][i];
   }
+#pragma unroll
+  for (int i = 0; i < kGroupsPerThread; ++i)
+    if (group_live(i)) store_out(i, s[i]);
   reset_counter(counters + strip * kCounterStride);
 }
 
@@ -225,8 +263,10 @@ int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, i
   if (M == 0 || N == 0) return G16_OK;
   if (ksplit < 1 || ksplit > 4096) return G16_E_SPLIT;
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return G16_E_NULL;
-  if (!aligned16(A) || !aligned16(B)) return G16_E_ALIGN;
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return G16_E_ALIGN;
   const Split sp = split_for(K, ksplit);
+  // the split partials are addressed through one buffer descriptor: 32-bit byte offsets
+  if (workspace_bytes(M, N, sp.ksplit) > 0x7fffffffu) return G16_E_SPLIT;
   const int nstrips = ceil_div(N, kStripCols);
   float* part = nullptr;
   uint32_t* counters = nullptr;
@@ -247,30 +287,26 @@ int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, i
 }  // namespace g16
 
 extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
-  // One 8-wavefront workgroup per CU for M <= 2 and per two CUs for larger M, each wavefront
-  // streaming >= kMinRows rows. Measured over split factors 4-64 (graph-timed, weights rotated
-  // past the Infinity Cache): one per CU is 3-22 % faster at M = 1, 2 for K x N = 4096^2,
-  // 11008 x 4096 and 8192^2 (1 x 8192^2: 30.5 -> 23.7 us); at M = 4 the extra slices cost more
-  // in the split reduction (4096^2: 13.3 vs 16.2 us).
+  // Up to one 8-wavefront workgroup per CU, rounded down so that no workgroups are left for a
+  // second round (1 x 4096 x 14336: 280 workgroups 28.9 us, 224 workgroups 21.9 us), each
+  // wavefront streaming >= min_rows rows; then, within a factor of two below that, a split that
+  // gives every wavefront whole blocks of rows_in_flight() rows (1 x 4096 x 12288: 8 slices
+  // 18.5 us, 10 slices 19.8 us; 4 x 4096^2: 16 slices 13.1 us, 32 slices 14.9 us). Chosen from
+  // graph-timed sweeps of 4-64 slices over M = 1..8 and K x N in {4096^2, 4096 x 11008,
+  // 4096 x 14336, 11008 x 4096}, weights rotated past the Infinity Cache.
   if (N <= 0 || K <= 0 || num_cus <= 0) return 1;
   const int nstrips = g16::ceil_div(N, g16::kStripCols);
-  // M <= 2 rounds down so that the grid never exceeds one workgroup per CU: a few workgroups past
-  // that run as a second round after the first (1 x 4096 x 14336 at 280 workgroups: 28.9 us;
-  // at 224: 21.9 us).
-  int ks = M <= 2 ? num_cus / nstrips : g16::ceil_div((num_cus + 1) / 2, nstrips);
+  int ks = num_cus / nstrips;
   // M = 1 keeps a full 16-row block per wavefront (6.3 vs 7.2 us at 1x1024x3072); larger M gain
   // more from the extra slices than they lose to a partial block (10.8 vs 11.3 us at 4x1024x3072).
   const int min_rows = M == 1 ? 16 : g16::kMinRows;
   const int cap = K / (g16::kWaves * min_rows) > 1 ? K / (g16::kWaves * min_rows) : 1;
   ks = ks < 1 ? 1 : (ks > cap ? cap : ks);
-  if (M <= 2) {
-    // Prefer a split that gives every wavefront whole blocks of rows_in_flight() = 16 rows, if one
-    // is within a factor of two (1 x 4096 x 12288: 8 slices 18.5 us, 10 slices 19.8 us).
-    for (int d = ks; d > ks / 2; --d) {
-      if (K % (g16::kWaves * 16 * d) == 0) {
-        ks = d;
-        break;
-      }
+  const int block = M == 4 ? g16::rows_in_flight<4>() : g16::rows_in_flight<1>();
+  for (int d = ks; d >= 1 && 2 * d >= ks; --d) {
+    if (K % (g16::kWaves * block * d) == 0) {
+      ks = d;
+      break;
     }
   }
   return g16::split_for(K, ks).ksplit;

@@ -144,6 +144,7 @@ int g16_hgemm_plan(int M, int N, int K, int num_cus);
  * A is read with 16-byte alignment (A must be 16-byte aligned, like B).
  * The kernel streams B once with 16-byte loads; K is split over ksplit workgroups per 512-column
  * strip and reduced deterministically (last arriving workgroup, slice order). C needs no zero-fill.
+ * The split workspace (ksplit * M * N * 4 bytes) must stay below 2 GiB (G16_E_SPLIT otherwise).
  * g16_skinny_plan() returns the ksplit this library would choose for num_cus compute units.
  */
 int g16_skinny_f32in(const float* A, const uint16_t* B, float* C, const float* bias, int M, int N,

@@ -49,6 +49,9 @@ def test_argument_errors_need_no_gpu(lib):
     assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, 64, 64, 1024, 0, None, 0, None, 0, None) == -5
     assert lib.g16_skinny_f32in(A, A, A, None, 9, 64, 64, 1, None, 0, None, 0, None) == -1   # M > 8
     assert lib.g16_skinny_f32in(A, A, A, None, 4, 4096, 4096, 8, A, 1 << 30, None, 0, None) == -4
+    assert lib.g16_skinny_f32in(A, A, A + 4, None, 1, 64, 64, 1, None, 0, None, 0, None) == -2  # C alignment
+    # split partials beyond a 2 GiB workspace (8 x 65536 x 1024 slices x 4 bytes) are refused
+    assert lib.g16_skinny_f32in(A, A, A, None, 8, 65536, 8192, 1024, A, 1 << 40, A, 1 << 20, None) == -5
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, 1000.0, None) == -1               # threshold not 2^k
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, -1024.0, None) == -1
 
