@@ -11,8 +11,8 @@
 //     (64 lanes x 16 bytes = 512 fp16 columns), so every load is fully coalesced and the
 //     activation A[m,k] it multiplies is the same for the whole wavefront: A comes in through
 //     scalar loads, and the vector memory path carries nothing but B.
-//   * Each lane issues 16 (32 for M = 4) row loads before it uses any, so a workgroup has 128 KB
-//     (256 KB) of B in flight: enough to cover HBM latency with a workgroup on every other CU. The
+//   * Each lane issues 16 row loads before it uses any, so a workgroup has 128 KB of B in flight:
+//     enough to cover HBM latency with up to one workgroup per CU. The
 //     weight is read exactly once, so the loads are non-temporal (measured 7-8 % faster at
 //     4096x4096).
 //   * Reduction is fixed-order: the wavefronts' partial rows are added in wavefront order through
@@ -32,10 +32,11 @@ constexpr int kWaves = 8;        // wavefronts per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMinRows = 8;      // the plan gives every wavefront at least this many rows
 
-// Rows each lane loads before using any (16 KB of B per wavefront at 16): 32 measured best for
-// M = 4 (13.0 vs 15.1 us at 4x4096x4096), 16 for M = 1, 2 and 8.
+// Rows each lane loads before using any (16 KB of B per wavefront). 16 for every M: with the
+// one-round LDS sum and the plan below, 32 rows at M = 4 lost to 16 (4 x 4096^2: 13.7 vs 12.5 us;
+// 4 x 1024 x 3072: 10.2 vs 7.8 us), M = 3 and 5 were unchanged.
 template <int MM>
-constexpr int rows_in_flight() { return MM == 4 ? 32 : 16; }
+constexpr int rows_in_flight() { return 16; }
 
 __device__ inline float x_at(const float* __restrict__ A, size_t i) { return A[i]; }
 // fp16 activations are read as the aligned dword holding them, so the (wavefront-uniform) load
@@ -291,7 +292,7 @@ extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
   // second round (1 x 4096 x 14336: 280 workgroups 28.9 us, 224 workgroups 21.9 us), each
   // wavefront streaming >= min_rows rows; then, within a factor of two below that, a split that
   // gives every wavefront whole blocks of rows_in_flight() rows (1 x 4096 x 12288: 8 slices
-  // 18.5 us, 10 slices 19.8 us; 4 x 4096^2: 16 slices 13.1 us, 32 slices 14.9 us). Chosen from
+  // 18.5 us, 10 slices 19.8 us). Chosen from
   // graph-timed sweeps of 4-64 slices over M = 1..8 and K x N in {4096^2, 4096 x 11008,
   // 4096 x 14336, 11008 x 4096}, weights rotated past the Infinity Cache.
   if (N <= 0 || K <= 0 || num_cus <= 0) return 1;
@@ -302,7 +303,7 @@ extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
   const int min_rows = M == 1 ? 16 : g16::kMinRows;
   const int cap = K / (g16::kWaves * min_rows) > 1 ? K / (g16::kWaves * min_rows) : 1;
   ks = ks < 1 ? 1 : (ks > cap ? cap : ks);
-  const int block = M == 4 ? g16::rows_in_flight<4>() : g16::rows_in_flight<1>();
+  const int block = g16::rows_in_flight<1>();  // the same for every M
   for (int d = ks; d >= 1 && 2 * d >= ks; --d) {
     if (K % (g16::kWaves * block * d) == 0) {
       ks = d;
