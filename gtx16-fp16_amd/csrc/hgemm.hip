@@ -330,9 +330,14 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
 #pragma unroll
     for (int f = 0; f < KS * (TM + TN); ++f) frag_op(buf, st, f);
   };
-  // MFMA m of a step: m = (ks * TM + i) * TN + j
+  // MFMA m of a step: m = (ks * TM + i) * TN + jj, with j = jj on even i and TN - 1 - jj on odd i
+  // (a snake over the blocks), so that consecutive MFMAs always share one operand register: the
+  // A fragment within a row of blocks, the B fragment across the turn. The part is power-limited
+  // on random operands and the MFMA's power grows with the operand bits that toggle between
+  // instructions: measured ~1 % faster than the plain row order at 4096^3, same result bits (every
+  // accumulator still receives its MFMAs in K order).
   auto mfma_op = [&](int buf, int m) {
-    const int ks = m / (TM * TN), i = (m / TN) % TM, j = m % TN;
+    const int ks = m / (TM * TN), i = (m / TN) % TM, jj = m % TN, j = (i & 1) ? TN - 1 - jj : jj;
     if constexpr (Cfg::MF16)
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
     else
