@@ -659,11 +659,14 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
 }  // namespace g16
 
 extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
-  // Split K when the output tiles cannot give every CU a workgroup (slice sizes below).
+  // Split K when the output tiles leave CUs without a workgroup, into as many slices as keep the
+  // grid within one workgroup per CU (the split-K kernels hold one workgroup per CU: a grid past
+  // that runs a second round; 768 x 4096^2: 192 tiles unsplit 48 us, 2 slices 54 us;
+  // 512 x 4096^2: 128 tiles unsplit 44 us, 2 slices 36 us; 512 x 11008 x 4096: 104 vs 75 us).
   if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0) return 1;
   const g16::Plan p = g16::choose_tile(M, N, false);
   const int tiles = p.ntm * p.ntn;
-  if (tiles >= num_cus / 2 || K < 512) return 1;
+  if (tiles >= num_cus || K < 512) return 1;
   const g16::Plan q = g16::choose_tile(M, N, true);
   const int qtiles = q.ntm * q.ntn;
   if (qtiles != tiles) return 1;
@@ -673,7 +676,7 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   // 128x128 tile, whose 64 KB partials make the reduction dearer: 1024^3 14.2 us at 2 slices vs
   // 15.3 us at 4, 512^3 10.0 us unsplit vs 10.8 us at 2; 64x1024x1024 on the 64x128 tile is best at
   // its K/256 cap, 8.7 us at 4 vs 9.7 us at 2).
-  int ks = g16::ceil_div(num_cus, tiles);
+  int ks = num_cus / tiles;
   const int cap = K / (q.tile == g16::Tile::T128 ? 512 : 256);
   ks = ks > cap ? cap : ks;
   ks = ks > 8 ? 8 : ks;
