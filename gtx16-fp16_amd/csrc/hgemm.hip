@@ -159,7 +159,6 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
                                                          uint32_t* __restrict__ counters, int M, int N, int K,
                                                          int kchunk, int ksplit, int ntm, int ntn) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN, MB = Cfg::MB, MK = Cfg::MK;
-  static_assert(!(SPLITK && Cfg::MF16), "split-K publishes 32x32-block accumulators");
   constexpr int BK = Cfg::BK, NSTAGE = Cfg::NSTAGE;
   __shared__ __attribute__((aligned(1024))) unsigned char sA[NSTAGE][Cfg::A_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char sB[NSTAGE][Cfg::B_BYTES];
@@ -346,7 +345,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
 
   static_assert(NSTAGE >= 3, "three stages at least");
   constexpr int NMFMA = KS * TM * TN, NFRAG = KS * (TM + TN), NDMA = Cfg::DMA_PER_STEP;
-  if constexpr (Cfg::WAVES == 8 && !SPLITK) {
+  if constexpr (Cfg::WAVES == 8) {
     // Ping-pong schedule for two wavefronts per SIMD. Wavefronts 0-3 (group 0) and 4-7 (group 1)
     // land one of each on every SIMD. Each wavefront alternates a memory phase M_j (fragment reads
     // of step j from LDS, DMA of step j+D into the ring) and a compute phase C_j (the 16 MFMAs of
@@ -441,54 +440,89 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // ---- split-K: publish this slice, let the last slice reduce ----
   if constexpr (SPLITK) {
     constexpr uint32_t TILE_BYTES = BM * BN * 4;
+    // Each wavefront stores its accumulators in its own register order: slot s of the wavefront is
+    // float4 piece q of accumulator (i, j), s = (i * TN + j) * QV + q.
+    constexpr int QV = sizeof(AccT) / sizeof(float4v);  // 4 for 32x32 blocks, 1 for 16x16 blocks
+    constexpr int SLOTS = TM * TN * QV;
+    auto piece = [&](int s) -> float4v {
+      const int b = s / QV, q = s % QV;
+      if constexpr (QV == 1) {
+        return acc[b / TN][b % TN];
+      } else {
+        const AccT& a = acc[b / TN][b % TN];
+        return float4v{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+      }
+    };
+    auto set_piece = [&](int s, float4v v) {
+      const int b = s / QV, q = s % QV;
+      if constexpr (QV == 1) {
+        acc[b / TN][b % TN] = v;
+      } else {
+        AccT& a = acc[b / TN][b % TN];
+        a[4 * q] = v.x;
+        a[4 * q + 1] = v.y;
+        a[4 * q + 2] = v.z;
+        a[4 * q + 3] = v.w;
+      }
+    };
     const __amdgpu_buffer_rsrc_t slices =
         coherent_rsrc(part + static_cast<size_t>(tile) * ksplit * (BM * BN), static_cast<uint32_t>(ksplit) * TILE_BYTES);
+    auto slot_off = [&](int z, int s) {
+      return static_cast<uint32_t>(z) * TILE_BYTES + static_cast<uint32_t>((wave * SLOTS + s) * 64 + lane) * 16u;
+    };
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t slot = (((wave * TM + i) * TN + j) * 4 + q) * 64 + lane;
-          store_coherent4(slices, static_cast<uint32_t>(z) * TILE_BYTES + slot * 16u,
-                          float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
-        }
+    for (int s = 0; s < SLOTS; ++s) store_coherent4(slices, slot_off(z, s), piece(s));
     if (!arrive_last_coherent(counters + tile * kCounterStride, static_cast<uint32_t>(ksplit))) return;
-    // Slices are added in slice order, ZB slices' loads in flight at a time (every slice, this
-    // one's included, is read back from the workspace).
-    constexpr int SLOTS = TM * TN * 4;
-    constexpr int ZB = (128 / (SLOTS * 4)) < 1 ? 1 : ((128 / (SLOTS * 4)) > 8 ? 8 : (128 / (SLOTS * 4)));
-    float4v sum[SLOTS];
+    // Slices are added in slice order (every slice, this one's included, is read back from the
+    // workspace), so each output is the same sum whichever slice arrives last.
+    if constexpr (SLOTS <= 16) {
+      // ZB slices' loads in flight at a time
+      constexpr int ZB = (128 / (SLOTS * 4)) < 1 ? 1 : ((128 / (SLOTS * 4)) > 8 ? 8 : (128 / (SLOTS * 4)));
+      float4v sum[SLOTS];
 #pragma unroll
-    for (int q = 0; q < SLOTS; ++q) sum[q] = float4v{0.f, 0.f, 0.f, 0.f};
-    for (int z0 = 0; z0 < ksplit; z0 += ZB) {
-      float4v v[ZB][SLOTS];
+      for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
+      for (int z0 = 0; z0 < ksplit; z0 += ZB) {
+        float4v v[ZB][SLOTS];
 #pragma unroll
-      for (int b = 0; b < ZB; ++b)
+        for (int b = 0; b < ZB; ++b)
 #pragma unroll
-        for (int q = 0; q < SLOTS; ++q) {
-          const uint32_t slot = static_cast<uint32_t>((wave * SLOTS + q) * 64 + lane);
-          v[b][q] = z0 + b < ksplit ? load_coherent4(slices, static_cast<uint32_t>(z0 + b) * TILE_BYTES + slot * 16u)
-                                    : float4v{0.f, 0.f, 0.f, 0.f};
+          for (int s = 0; s < SLOTS; ++s)
+            v[b][s] = z0 + b < ksplit ? load_coherent4(slices, slot_off(z0 + b, s)) : float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < ZB; ++b)
+#pragma unroll
+          for (int s = 0; s < SLOTS; ++s)
+            if (z0 + b < ksplit) sum[s] += v[b][s];
+      }
+#pragma unroll
+      for (int s = 0; s < SLOTS; ++s) set_piece(s, sum[s]);
+    } else {
+      // The 256x256 tile: its accumulators fill most of the register file, so the sums build up in
+      // the accumulators themselves, kCh slots at a time, two slices' loads in flight.
+      constexpr int kCh = 8;
+      static_assert(SLOTS % kCh == 0, "whole chunks");
+#pragma unroll
+      for (int c0 = 0; c0 < SLOTS; c0 += kCh) {
+        float4v s[kCh];
+#pragma unroll
+        for (int q = 0; q < kCh; ++q) s[q] = float4v{0.f, 0.f, 0.f, 0.f};
+        for (int z0 = 0; z0 < ksplit; z0 += 2) {
+          float4v v0[kCh], v1[kCh];
+#pragma unroll
+          for (int q = 0; q < kCh; ++q) {
+            v0[q] = load_coherent4(slices, slot_off(z0, c0 + q));
+            v1[q] = z0 + 1 < ksplit ? load_coherent4(slices, slot_off(z0 + 1, c0 + q)) : float4v{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+          for (int q = 0; q < kCh; ++q) {
+            s[q] += v0[q];
+            if (z0 + 1 < ksplit) s[q] += v1[q];
+          }
         }
 #pragma unroll
-      for (int b = 0; b < ZB; ++b)
-#pragma unroll
-        for (int q = 0; q < SLOTS; ++q)
-          if (z0 + b < ksplit) sum[q] += v[b][q];
+        for (int q = 0; q < kCh; ++q) set_piece(c0 + q, s[q]);
+      }
     }
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4v t = sum[(i * TN + j) * 4 + q];
-          acc[i][j][4 * q] = t.x;
-          acc[i][j][4 * q + 1] = t.y;
-          acc[i][j][4 * q + 2] = t.z;
-          acc[i][j][4 * q + 3] = t.w;
-        }
     reset_counter(counters + tile * kCounterStride);
   }
 
@@ -557,15 +591,14 @@ struct Plan {
   int ntm, ntn;
 };
 
-// Split-K launches use the tiles up to 128x128 (the 256x256 tile has no split-K variant: its
-// accumulators fill the register file).
-Plan choose_tile(int M, int N, bool splitk) {
+// The same tile with or without a split: a split only spreads K over more workgroups.
+Plan choose_tile(int M, int N, bool /*splitk*/) {
   Plan p{};
   if (M <= 32) {
     p.tile = Tile::T32; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
     p.tile = Tile::T64; p.bm = 64; p.bn = 128;
-  } else if (!splitk && M >= 1024 && N >= 256 && static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256) >= 128) {
+  } else if (M >= 1024 && N >= 256 && static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256) >= 128) {
     p.tile = Tile::T256; p.bm = 256; p.bn = 256;
   } else {
     p.tile = Tile::T128; p.bm = 128; p.bn = 128;
@@ -596,6 +629,7 @@ GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b) {
   if (packed) return hgemm_kernel<Cfg256, OUT_F16, false, true>;
   if (splitk) {
     switch (t) {
+      case Tile::T256: return hgemm_kernel<Cfg256, OUT_F16, true>;
       case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, true>;
       case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, true>;
       default: return hgemm_kernel<Cfg32, OUT_F16, true>;
@@ -677,7 +711,11 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   // 15.3 us at 4, 512^3 10.0 us unsplit vs 10.8 us at 2; 64x1024x1024 on the 64x128 tile is best at
   // its K/256 cap, 8.7 us at 4 vs 9.7 us at 2).
   int ks = num_cus / tiles;
-  const int cap = K / (q.tile == g16::Tile::T128 ? 512 : 256);
+  // The 256x256 tile keeps >= 4096 K per slice: its 256 KB partials cost the exchange more than
+  // the idle CUs cost at shorter K (2048 x 4096 x 11008: 202 us unsplit, 184 us at 2 slices;
+  // 2048 x 8192 x 4096: 154 vs 147 us; but 2048 x 4096^2: 89.6 vs 89.7 us and 2048 x 2048 x 4096:
+  // 53 vs 63 us).
+  const int cap = K / (q.tile == g16::Tile::T256 ? 4096 : (q.tile == g16::Tile::T128 ? 512 : 256));
   ks = ks > cap ? cap : ks;
   ks = ks > 8 ? 8 : ks;
   return g16::ksplit_for(K, ks < 1 ? 1 : ks).ksplit;

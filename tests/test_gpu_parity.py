@@ -195,7 +195,9 @@ def test_massive_activations(g, cuda, M, in_dtype):
     assert oracle.rel_err(_np(y), ref) <= tol
 
 
-@pytest.mark.parametrize("M,K,N", [(64, 1024, 1024), (64, 4096, 1024), (1024, 1024, 1024), (33, 4096, 768)])
+# (1024, 1024, 8192) runs the 256x256 tile: 128 output tiles, split over its ping-pong schedule
+@pytest.mark.parametrize("M,K,N", [(64, 1024, 1024), (64, 4096, 1024), (1024, 1024, 1024), (33, 4096, 768),
+                                   (1024, 1024, 8192)])
 def test_splitk_deterministic_and_matches_plain(lib, cuda, M, K, N):
     a = randn((M, K), seed=0, dtype=torch.float16).to(cuda)
     b = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
