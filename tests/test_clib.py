@@ -65,6 +65,17 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_hgemm_plan(512, 512, 512, 256) == 1
     assert lib.g16_hgemm_plan(64, 1024, 1024, 256) == 4
     assert lib.g16_hgemm_plan(64, 1024, 4096, 256) == 8
+    # tiles that leave CUs idle split as far as one workgroup per CU allows
+    assert lib.g16_hgemm_plan(512, 4096, 4096, 256) == 2             # 128 tiles of 128x128
+    assert lib.g16_hgemm_plan(768, 4096, 4096, 256) == 1             # 192 tiles: 2 slices would overflow
+    # the 256x256 tile splits only with >= 4096 K per slice
+    assert lib.g16_hgemm_plan(2048, 4096, 4096, 256) == 1
+    assert lib.g16_hgemm_plan(2048, 4096, 8192, 256) == 2
+    assert lib.g16_hgemm_use_packed(2048, 4096, 8192, 256) == 0      # split shapes take the row-major cast
+    # skinny: whole 16-row blocks per wavefront, at most one workgroup per CU
+    assert lib.g16_skinny_plan(1, 4096, 4096, 256) == 32
+    assert lib.g16_skinny_plan(4, 4096, 4096, 256) == 32
+    assert lib.g16_skinny_plan(1, 14336, 4096, 256) == 8             # 28 strips: 8 x 28 <= 256
     ks = lib.g16_skinny_plan(4, 4096, 4096, 256)
     assert lib.g16_skinny_workspace_bytes(4, 4096, 4096, ks) == ks * 4 * 4096 * 4
     assert lib.g16_skinny_counter_bytes(4, 4096, 4096, ks) == (4096 // 512) * 256
