@@ -295,9 +295,12 @@ def test_skinny_matches_oracle(g, cuda, M, K, N, x_dtype, with_bias):
     assert oracle.rel_err(_np(y), ref) <= SKINNY_TOL
 
 
-@pytest.mark.parametrize("ksplit", [1, 2, 5, 16, 64])
-def test_skinny_explicit_splits_deterministic(lib, cuda, ksplit):
-    M, K, N = 4, 4096, 4096
+# M = 1 and 3 reduce single columns, M >= 4 four-column groups (two per thread at M = 8, a partial
+# second round of groups at M = 5)
+@pytest.mark.parametrize("M,ksplit", [(4, 1), (4, 2), (4, 5), (4, 16), (4, 64), (1, 32), (3, 7), (5, 16),
+                                      (8, 32), (8, 3)])
+def test_skinny_explicit_splits_deterministic(lib, cuda, M, ksplit):
+    K, N = 4096, 4096
     x = randn((M, K), seed=0).to(cuda)
     w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
     b = randn((N,), seed=2, scale=0.02).to(cuda)
