@@ -136,6 +136,7 @@ struct TileCfg {
 };
 
 using Cfg256 = TileCfg<256, 256, 32, 2, 4, 4, true>;  // 8 wavefronts (two per SIMD), 4-stage ring, 128 KB
+using Cfg256n = TileCfg<256, 128, 32, 2, 4, 4, true>;  // the same schedule on half the columns, 96 KB
 using Cfg128 = TileCfg<128, 128, 32, 2, 2, 4>;  // 64 KB: two workgroups per CU
 using Cfg64 = TileCfg<64, 128, 64, 1, 4, 4>;
 using Cfg32 = TileCfg<32, 128, 64, 1, 4, 4>;
@@ -196,7 +197,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // of DMA operations per step constant, which the vmcnt waits rely on.
   auto rsrc_a = [&](int k0) {
     if constexpr (PACKED_A) {
-      static_assert(Cfg::BM == 256 && Cfg::BK == 32 && !SPLITK, "packed A is the 256x256x32 stage image");
+      static_assert(Cfg::BM == 256 && Cfg::BK == 32 && !SPLITK, "packed A is the stage image of 256 rows x 32 K");
       return __builtin_amdgcn_make_buffer_rsrc(
           const_cast<_Float16*>(A) + static_cast<size_t>(tm) * ceil_div(K, BK) * (Cfg::A_BYTES / 2), 0, 0x7fffffff,
           kRawBufferDword3);
@@ -583,7 +584,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   }
 }
 
-enum class Tile { T256, T128, T64, T32 };
+enum class Tile { T256, T256N, T128, T64, T32 };
 
 struct Plan {
   Tile tile;
@@ -591,15 +592,34 @@ struct Plan {
   int ntm, ntn;
 };
 
-// The same tile with or without a split: a split only spreads K over more workgroups.
-Plan choose_tile(int M, int N, bool /*splitk*/) {
+// Compute units of the current device (cached per device; 256, the MI355X count, if the query fails).
+int device_cus() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    cache[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cache[dev];
+}
+
+// The same tile with or without a split: a split only spreads K over more workgroups. Large
+// outputs take the 256x256 tile once it gives more than half the CUs a workgroup; just below that
+// (3/8 to 1/2 of the CUs), the 256x128 tile on the same schedule fills them instead (2048 x 4096^2,
+// 128 tiles of 256^2 on 256 CUs: 89 us, 256 tiles of 256x128: 76-82 us; with 144 tiles of 256^2
+// the 256x128 grid would overflow the CUs: 93 vs 128 us).
+Plan choose_tile(int M, int N, bool /*splitk*/, int num_cus) {
   Plan p{};
+  const long t256 = static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256);
   if (M <= 32) {
     p.tile = Tile::T32; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
     p.tile = Tile::T64; p.bm = 64; p.bn = 128;
-  } else if (M >= 1024 && N >= 256 && static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256) >= 128) {
+  } else if (M >= 1024 && N >= 256 && 2 * t256 > num_cus) {
     p.tile = Tile::T256; p.bm = 256; p.bn = 256;
+  } else if (M >= 1024 && N >= 256 && 8 * t256 > 3 * num_cus) {
+    p.tile = Tile::T256N; p.bm = 256; p.bn = 128;
   } else {
     p.tile = Tile::T128; p.bm = 128; p.bn = 128;
   }
@@ -626,10 +646,11 @@ using GemmFn = void (*)(const _Float16*, const _Float16*, void*, const float*, c
 template <bool OUT_F16>
 GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b) {
   if (packed_b) return hgemm_kernel<Cfg256, OUT_F16, false, true, true>;
-  if (packed) return hgemm_kernel<Cfg256, OUT_F16, false, true>;
+  if (packed) return t == Tile::T256N ? hgemm_kernel<Cfg256n, OUT_F16, false, true> : hgemm_kernel<Cfg256, OUT_F16, false, true>;
   if (splitk) {
     switch (t) {
       case Tile::T256: return hgemm_kernel<Cfg256, OUT_F16, true>;
+      case Tile::T256N: return hgemm_kernel<Cfg256n, OUT_F16, true>;
       case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, true>;
       case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, true>;
       default: return hgemm_kernel<Cfg32, OUT_F16, true>;
@@ -637,6 +658,7 @@ GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b) {
   }
   switch (t) {
     case Tile::T256: return hgemm_kernel<Cfg256, OUT_F16, false>;
+    case Tile::T256N: return hgemm_kernel<Cfg256n, OUT_F16, false>;
     case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, false>;
     case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, false>;
     default: return hgemm_kernel<Cfg32, OUT_F16, false>;
@@ -663,9 +685,11 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return G16_E_NULL;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return G16_E_ALIGN;
   const KSplit ks = ksplit_for(K, ksplit);
-  Plan p = choose_tile(M, N, ks.ksplit > 1);
-  if (packed) {  // the packed layout is the 256x256 tile's stage image: always that tile, no split
-    p = Plan{Tile::T256, 256, 256, ceil_div(M, 256), ceil_div(N, 256)};
+  Plan p = choose_tile(M, N, ks.ksplit > 1, device_cus());
+  if (packed) {
+    // the packed A layout is the stage image of the 256-row tiles: the 256x256 tile, or the
+    // 256x128 one where the plan picks it; a packed weight pairs with the 256x256 tile only
+    if (packed_b || p.tile != Tile::T256N) p = Plan{Tile::T256, 256, 256, ceil_div(M, 256), ceil_div(N, 256)};
   }
   float* part = nullptr;
   uint32_t* counters = nullptr;
@@ -677,7 +701,7 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
     part = static_cast<float*>(ws);
   }
   const dim3 grid(static_cast<unsigned>(p.ntm * p.ntn), static_cast<unsigned>(ks.ksplit)),
-      block(p.tile == Tile::T256 ? Cfg256::THREADS : 256);
+      block(p.tile == Tile::T256 || p.tile == Tile::T256N ? Cfg256::THREADS : 256);
   const auto* a = reinterpret_cast<const _Float16*>(A);
   const auto* b = reinterpret_cast<const _Float16*>(B);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -698,10 +722,10 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   // that runs a second round; 768 x 4096^2: 192 tiles unsplit 48 us, 2 slices 54 us;
   // 512 x 4096^2: 128 tiles unsplit 44 us, 2 slices 36 us; 512 x 11008 x 4096: 104 vs 75 us).
   if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0) return 1;
-  const g16::Plan p = g16::choose_tile(M, N, false);
+  const g16::Plan p = g16::choose_tile(M, N, false, num_cus);
   const int tiles = p.ntm * p.ntn;
   if (tiles >= num_cus || K < 512) return 1;
-  const g16::Plan q = g16::choose_tile(M, N, true);
+  const g16::Plan q = g16::choose_tile(M, N, true, num_cus);
   const int qtiles = q.ntm * q.ntn;
   if (qtiles != tiles) return 1;
   // At most 8 slices: the last slice to arrive reads every other slice's fp32 tile at one CU's
@@ -711,11 +735,13 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   // 15.3 us at 4, 512^3 10.0 us unsplit vs 10.8 us at 2; 64x1024x1024 on the 64x128 tile is best at
   // its K/256 cap, 8.7 us at 4 vs 9.7 us at 2).
   int ks = num_cus / tiles;
-  // The 256x256 tile keeps >= 4096 K per slice: its 256 KB partials cost the exchange more than
-  // the idle CUs cost at shorter K (2048 x 4096 x 11008: 202 us unsplit, 184 us at 2 slices;
-  // 2048 x 8192 x 4096: 154 vs 147 us; but 2048 x 4096^2: 89.6 vs 89.7 us and 2048 x 2048 x 4096:
-  // 53 vs 63 us).
-  const int cap = K / (q.tile == g16::Tile::T256 ? 4096 : (q.tile == g16::Tile::T128 ? 512 : 256));
+  // The 256-row tiles keep >= 4096 K per slice: their 256 KB partials cost the exchange more than
+  // idle CUs cost at shorter K (measured on 128 tiles of 256x256: 2048 x 4096 x 11008 202 us
+  // unsplit, 184 us at 2 slices; 2048 x 4096^2 89.6 vs 89.7 us; 2048 x 2048 x 4096 53 vs 63 us).
+  // choose_tile now gives those shapes 256x128 tiles that fill the CUs instead, so the planner
+  // does not split the 256-row tiles; explicit splits (g16_hgemm_splitk) still run them.
+  const bool big = q.tile == g16::Tile::T256 || q.tile == g16::Tile::T256N;
+  const int cap = K / (big ? 4096 : (q.tile == g16::Tile::T128 ? 512 : 256));
   ks = ks > cap ? cap : ks;
   ks = ks > 8 ? 8 : ks;
   return g16::ksplit_for(K, ks < 1 ? 1 : ks).ksplit;
@@ -724,14 +750,14 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
 extern "C" size_t g16_hgemm_splitk_workspace_bytes(int M, int N, int K, int ksplit) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const g16::KSplit ks = g16::ksplit_for(K, ksplit);
-  const g16::Plan p = g16::choose_tile(M, N, ks.ksplit > 1);
+  const g16::Plan p = g16::choose_tile(M, N, ks.ksplit > 1, g16::device_cus());
   return g16::splitk_ws_bytes(p, ks.ksplit);
 }
 
 extern "C" size_t g16_hgemm_splitk_counter_bytes(int M, int N, int K, int ksplit) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const g16::KSplit ks = g16::ksplit_for(K, ksplit);
-  const g16::Plan p = g16::choose_tile(M, N, ks.ksplit > 1);
+  const g16::Plan p = g16::choose_tile(M, N, ks.ksplit > 1, g16::device_cus());
   return g16::splitk_counter_bytes(p, ks.ksplit);
 }
 
@@ -748,7 +774,14 @@ extern "C" int g16_hgemm_f16out(const uint16_t* A, const uint16_t* B, uint16_t* 
 extern "C" int g16_hgemm_use_packed(int M, int N, int K, int num_cus) {
   // The packed route pays off where the plain plan already picks the 256x256 tile without a split.
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return g16::choose_tile(M, N, false).tile == g16::Tile::T256 && g16_hgemm_plan(M, N, K, num_cus) == 1 ? 1 : 0;
+  const g16::Tile t = g16::choose_tile(M, N, false, num_cus).tile;
+  return (t == g16::Tile::T256 || t == g16::Tile::T256N) && g16_hgemm_plan(M, N, K, num_cus) == 1 ? 1 : 0;
+}
+
+extern "C" int g16_hgemm_use_packed_b(int M, int N, int K, int num_cus) {
+  // A prepacked weight (g16_pack_weight) is the 256x256 tile's B stage image: it serves the packed
+  // route where that route runs the 256x256 tile.
+  return g16_hgemm_use_packed(M, N, K, num_cus) && g16::choose_tile(M, N, false, num_cus).tile == g16::Tile::T256 ? 1 : 0;
 }
 
 extern "C" int g16_hgemm_packed_f32out(const uint16_t* Ap, const uint16_t* B, float* C, const float* bias,

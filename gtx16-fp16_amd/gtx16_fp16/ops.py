@@ -211,8 +211,10 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
 
 
 def prepacked_route(M: int, N: int, K: int, device: torch.device) -> bool:
-    """True where mm_t takes the tile-packed 256x256 route, the one a prepacked weight serves."""
-    return _gemm_route(_clib.load(), M, N, K, device)[0] == "packed"
+    """True where mm_t takes the tile-packed route on the 256x256 tile, the one a prepacked weight
+    serves."""
+    return _gemm_route(_clib.load(), M, N, K, device)[0] == "packed" and \
+        _clib.load().g16_hgemm_use_packed_b(M, N, K, _sm_count(device)) == 1
 
 
 def pack_weight(w_t: torch.Tensor) -> torch.Tensor:

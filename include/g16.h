@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 7
+#define G16_ABI_VERSION 8
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -84,14 +84,15 @@ int g16_hgemm_f16out(const uint16_t* A, const uint16_t* B, uint16_t* C, const fl
  * Tile-packed route for the large GEMM: the same two reference kernels as above, rowscale_f32 /
  * rowscale_f16 (src/gtx16_fp16/kernels.py:227-250) then hgemm_f32out / hgemm_f16out
  * (kernels.py:139-142,148-151), as launched by src/gtx16_fp16/ops.py:86-90,103-108, with the fp16
- * intermediate written in a layout the 256x256 GEMM tile streams as contiguous 16 KB blocks instead
- * of row-major. Same values, same results bit for bit; only the intermediate's layout differs.
+ * intermediate written in a layout the 256-row GEMM tiles (256x256, and 256x128 where the plan
+ * picks it) stream as contiguous 16 KB blocks instead of row-major. Same values, same results bit
+ * for bit; only the intermediate's layout differs.
  *   Packed layout of Yp: blocks of 256 rows x 32 columns, block (tm, ks) at block index
  *   tm * ceil(K/32) + ks, 16 KB each; inside a block, 16-byte chunk q*64 + i (q < 16, i < 64)
  *   holds columns 8*((i % 4) ^ ((r / 2) % 4)) .. +7 of local row r = 16q + i/4. Rows >= M and
  *   columns >= K are written as zeros. g16_packed_a_bytes() gives the size.
- * g16_hgemm_use_packed() is 1 where mm_t takes this route (the plain plan would use the 256x256
- * tile without a split), else 0. The packed GEMM accepts any shape.
+ * g16_hgemm_use_packed() is 1 where mm_t takes this route (the plain plan would use a 256-row tile
+ * without a split), else 0. The packed GEMM accepts any shape.
  */
 size_t g16_packed_a_bytes(int M, int K);
 int g16_rowscale_pack_f32(const float* X, uint16_t* Yp, float* S, int M, int K, float thresh,
@@ -110,6 +111,8 @@ int g16_hgemm_use_packed(int M, int N, int K, int num_cus);
  * linear.py:30-37). g16_pack_weight writes w_t transposed ([N,K]) in the tile-packed layout above
  * (rows = N); g16_hgemm_packed_ab_* is the 256x256 GEMM with both operands packed. Same values and
  * the same result bits as g16_hgemm_packed_* on the unpacked weight.
+ * g16_hgemm_use_packed_b() is 1 where the packed route runs the 256x256 tile, the one a packed
+ * weight serves (elsewhere the packed route runs the 256x128 tile on the unpacked weight).
  */
 size_t g16_packed_b_bytes(int K, int N);
 int g16_pack_weight(const uint16_t* w_t, uint16_t* wp, int K, int N, void* stream);
@@ -118,6 +121,7 @@ int g16_hgemm_packed_ab_f32out(const uint16_t* Ap, const uint16_t* Bp, float* C,
 int g16_hgemm_packed_ab_f16out(const uint16_t* Ap, const uint16_t* Bp, uint16_t* C,
                                const float* bias, const float* rscale, int M, int N, int K,
                                void* stream);
+int g16_hgemm_use_packed_b(int M, int N, int K, int num_cus);
 
 /* ---------------------------------------------------------------------------------------------
  * Deterministic split-K GEMM for shapes with too few output tiles to fill the GPU.

@@ -435,7 +435,9 @@ def test_rowscale_pack_bitexact(lib, cuda, M, K, in_dtype):
     assert np.array_equal(_np(s).view(np.uint32), S.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,K,N", [(300, 136, 264), (2300, 264, 4096), (4096, 4096, 4096), (4100, 1000, 2056)])
+# (2048, 512, 4096) and the ragged (1800, 136, 3896) give 128 tiles of 256x256: they run 256x128 tiles
+@pytest.mark.parametrize("M,K,N", [(300, 136, 264), (2300, 264, 4096), (4096, 4096, 4096), (4100, 1000, 2056),
+                                   (2048, 512, 4096), (1800, 136, 3896)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 def test_packed_gemm_bitwise_equals_rowmajor(lib, cuda, M, K, N, out_dtype):
     # outlier rows still need the pow2 rescale, but stay small enough that an fp16 output is finite
@@ -453,8 +455,8 @@ def test_packed_gemm_bitwise_equals_rowmajor(lib, cuda, M, K, N, out_dtype):
     c_pk = torch.empty(M, N, dtype=out_dtype, device=cuda)
     fn_row = lib.g16_hgemm_f16out if f16 else lib.g16_hgemm_f32out
     fn_pk = lib.g16_hgemm_packed_f16out if f16 else lib.g16_hgemm_packed_f32out
-    # both on the 256x256 tile where the plain plan picks it; elsewhere the row-major GEMM uses a
-    # smaller tile and only the oracle bar applies
+    # both on the same 256-row tile where the plain plan picks one; elsewhere the row-major GEMM
+    # uses a smaller tile and only the oracle bar applies
     assert fn_row(y16.data_ptr(), w.data_ptr(), c_row.data_ptr(), bias.data_ptr(), s.data_ptr(), M, N, K, st) == 0
     assert fn_pk(yp.data_ptr(), w.data_ptr(), c_pk.data_ptr(), bias.data_ptr(), sp.data_ptr(), M, N, K, st) == 0
     torch.cuda.synchronize()

@@ -20,14 +20,15 @@ def _ceil(a: int, b: int) -> int:
     return -(-a // b)
 
 
-def _tiles(M: int, N: int) -> int:
-    # the library's tile choice (choose_tile): 32x128, 64x128, 256x256 or 128x128
-    if M <= 32:
-        return _ceil(N, 128)
+def _tiles(M: int, N: int, num_cus: int) -> int:
+    # the library's tile choice (choose_tile): 32x128, 64x128, 256x256, 256x128 or 128x128
     if M <= 64:
         return _ceil(N, 128)
-    if M >= 1024 and N >= 256 and _ceil(M, 256) * _ceil(N, 256) >= 128:
-        return _ceil(M, 256) * _ceil(N, 256)
+    t256 = _ceil(M, 256) * _ceil(N, 256)
+    if M >= 1024 and N >= 256 and 2 * t256 > num_cus:
+        return t256
+    if M >= 1024 and N >= 256 and 8 * t256 > 3 * num_cus:
+        return _ceil(M, 256) * _ceil(N, 128)
     return _ceil(M, 128) * _ceil(N, 128)
 
 
@@ -39,7 +40,7 @@ cus = st.sampled_from([64, 120, 256, 304])
 @given(M=st.integers(min_value=9, max_value=70000), N=dims, K=dims, num_cus=cus)
 def test_gemm_plan_limits(lib, M, N, K, num_cus):
     ks = lib.g16_hgemm_plan(M, N, K, num_cus)
-    tiles = _tiles(M, N)
+    tiles = _tiles(M, N, num_cus)
     assert 1 <= ks <= 8
     if ks > 1:
         # split only when tiles leave CUs idle, never past one workgroup per CU, >= 256 K a slice
