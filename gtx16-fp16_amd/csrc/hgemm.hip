@@ -730,10 +730,11 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   if (qtiles != tiles) return 1;
   // At most 8 slices: the last slice to arrive reads every other slice's fp32 tile at one CU's
   // bandwidth, so beyond ~8 the reduction costs more than the extra parallelism gains (measured:
-  // 64x4096x1024 12.1 us at 8 vs 14.3 us at 16). Each slice keeps >= 256 K (>= 512 K for the
-  // 128x128 tile, whose 64 KB partials make the reduction dearer: 1024^3 14.2 us at 2 slices vs
-  // 15.3 us at 4, 512^3 10.0 us unsplit vs 10.8 us at 2; 64x1024x1024 on the 64x128 tile is best at
-  // its K/256 cap, 8.7 us at 4 vs 9.7 us at 2).
+  // 64x4096x1024 12.1 us at 8 vs 14.3 us at 16). Each slice keeps >= 256 K (>= 1024 K for the
+  // 128x128 tile, whose 64 KB partials make the reduction dearer; graph-timed: 1024^3 13.2 us
+  // unsplit vs 14.3 at 2 slices, 1024 x 1024 x 2048 14.1 vs 17.2, but 1024 x 2048 x 1024 18.1 at 2
+  // slices vs 21.1 unsplit and 20.2 at 4; 64x1024x1024 on the 64x128 tile is best at its K/256 cap,
+  // 8.7 us at 4 vs 9.7 us at 2).
   int ks = num_cus / tiles;
   // The 256-row tiles keep >= 4096 K per slice: their 256 KB partials cost the exchange more than
   // idle CUs cost at shorter K (measured on 128 tiles of 256x256: 2048 x 4096 x 11008 202 us
@@ -741,7 +742,7 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   // choose_tile now gives those shapes 256x128 tiles that fill the CUs instead, so the planner
   // does not split the 256-row tiles; explicit splits (g16_hgemm_splitk) still run them.
   const bool big = q.tile == g16::Tile::T256 || q.tile == g16::Tile::T256N;
-  const int cap = K / (big ? 4096 : (q.tile == g16::Tile::T128 ? 512 : 256));
+  const int cap = K / (big ? 4096 : (q.tile == g16::Tile::T128 ? 1024 : 256));
   ks = ks > cap ? cap : ks;
   ks = ks > 8 ? 8 : ks;
   return g16::ksplit_for(K, ks < 1 ? 1 : ks).ksplit;

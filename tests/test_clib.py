@@ -60,8 +60,9 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_skinny_plan(1, 4096, 4096, 256) >= 8
     assert lib.g16_hgemm_plan(4096, 4096, 4096, 256) == 1           # enough tiles: no split
     assert lib.g16_hgemm_plan(64, 1024, 4096, 256) > 1              # few tiles: split K
-    # measured-best splits: >= 512 K per slice on the 128x128 tile, >= 256 K on the 64x128 tile
-    assert lib.g16_hgemm_plan(1024, 1024, 1024, 256) == 2
+    # measured-best splits: >= 1024 K per slice on the 128x128 tile, >= 256 K on the 64x128 tile
+    assert lib.g16_hgemm_plan(1024, 1024, 1024, 256) == 1
+    assert lib.g16_hgemm_plan(1024, 1024, 2048, 256) == 2
     assert lib.g16_hgemm_plan(512, 512, 512, 256) == 1
     assert lib.g16_hgemm_plan(64, 1024, 1024, 256) == 4
     assert lib.g16_hgemm_plan(64, 1024, 4096, 256) == 8
