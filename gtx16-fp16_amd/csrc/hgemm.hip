@@ -811,3 +811,50 @@ extern "C" int g16_hgemm_splitk(const uint16_t* A, const uint16_t* B, void* C, i
   return g16::gemm_launch(A, B, C, c_is_f16 != 0, bias, rscale, M, N, K, ksplit, workspace, workspace_bytes, counters,
                           counter_bytes, stream);
 }
+
+namespace g16 {
+namespace {
+
+// The fp16 cast and the row scales share one scratch buffer: [cast, padded to 256 bytes][M floats].
+size_t cast_bytes(int M, int K, bool packed) {
+  return packed ? packed_bytes_for(M, K) : static_cast<size_t>(M) * K * 2;
+}
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+
+}  // namespace
+}  // namespace g16
+
+extern "C" size_t g16_mm_t_scratch_bytes(int M, int N, int K, int num_cus) {
+  if (M <= 0 || N <= 0 || K < 0) return 0;
+  const bool packed = g16_hgemm_use_packed(M, N, K, num_cus) == 1;
+  return g16::round256(g16::cast_bytes(M, K, packed)) + static_cast<size_t>(M) * sizeof(float);
+}
+
+extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, void* out, int out_is_f16,
+                             const float* bias, float thresh, int M, int N, int K, int num_cus, void* scratch,
+                             size_t scratch_bytes, void* workspace, size_t workspace_bytes, uint32_t* counters,
+                             size_t counter_bytes, void* stream) {
+  // mm_t's GEMM path in one call: the same two launches, and the same result bits, as the
+  // separate rowscale and GEMM entry points on the route g16_hgemm_use_packed / g16_hgemm_plan pick
+  if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0 || num_cus <= 0) return G16_E_SHAPE;
+  if (M == 0 || N == 0) return G16_OK;
+  if (scratch == nullptr || out == nullptr || (K > 0 && (x == nullptr || w_t == nullptr))) return G16_E_NULL;
+  if (!g16::aligned16(scratch)) return G16_E_ALIGN;
+  if (scratch_bytes < g16_mm_t_scratch_bytes(M, N, K, num_cus)) return G16_E_WORKSPACE;
+  const bool packed = g16_hgemm_use_packed(M, N, K, num_cus) == 1;
+  auto* y = static_cast<uint16_t*>(scratch);
+  auto* s = reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + g16::round256(g16::cast_bytes(M, K, packed)));
+  int st;
+  if (x_is_f32)
+    st = packed ? g16_rowscale_pack_f32(static_cast<const float*>(x), y, s, M, K, thresh, stream)
+                : g16_rowscale_f32(static_cast<const float*>(x), y, s, M, K, thresh, stream);
+  else
+    st = packed ? g16_rowscale_pack_f16(static_cast<const uint16_t*>(x), y, s, M, K, thresh, stream)
+                : g16_rowscale_f16(static_cast<const uint16_t*>(x), y, s, M, K, thresh, stream);
+  if (st != G16_OK) return st;
+  if (packed)
+    return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true);
+  const int ks = g16_hgemm_plan(M, N, K, num_cus);
+  return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, ks, workspace, workspace_bytes, counters,
+                          counter_bytes, stream);
+}

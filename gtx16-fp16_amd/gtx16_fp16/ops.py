@@ -83,19 +83,22 @@ _routes: dict[tuple[int, int, int, int], tuple] = {}
 
 
 def _gemm_route(lib, M: int, N: int, K: int, dev: torch.device) -> tuple:
+    """(route, scratch bytes, ksplit, split workspace bytes, split counter bytes) of the GEMM path
+    for this shape: the plan g16_mm_t_gemm follows for the same compute-unit count."""
     key = (M, N, K, dev.index or 0)
     r = _routes.get(key)
     if r is None:
         cus = _sm_count(dev)
+        scratch = lib.g16_mm_t_scratch_bytes(M, N, K, cus)
         if lib.g16_hgemm_use_packed(M, N, K, cus):
-            r = ("packed", lib.g16_packed_a_bytes(M, K))
+            r = ("packed", scratch, 1, 0, 0)
         else:
             ksplit = lib.g16_hgemm_plan(M, N, K, cus)
             if ksplit > 1:
-                r = ("splitk", ksplit, lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit),
+                r = ("splitk", scratch, ksplit, lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit),
                      lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit))
             else:
-                r = ("plain",)
+                r = ("plain", scratch, 1, 0, 0)
         _remember(key, r)
     return r
 
@@ -179,34 +182,17 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
                     "skinny GEMM")
         return out if out_dtype == torch.float32 else out.to(out_dtype)
 
-    # GEMM path: fp16 inputs, with per-row power-of-two scaling for rows that would overflow.
-    route = _gemm_route(lib, M, N, K, dev)
+    # GEMM path: fp16 inputs, with per-row power-of-two scaling for rows that would overflow. One
+    # library call runs the rowscale cast into `scratch` and the GEMM on the planned route: the
+    # tile-packed 256-row tiles for large outputs, split-K where the tiles leave CUs idle, else the
+    # plain tiles (the cast, scales and GEMM of ops.py:86-108).
+    kind, scratch_bytes, _ks, ws_bytes, cnt_bytes = _gemm_route(lib, M, N, K, dev)
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
-    f32in = x2d.dtype == torch.float32
-    if route[0] == "packed":
-        # Large GEMM: the cast writes the fp16 copy straight into the tile-packed layout the
-        # 256x256 kernel streams (same values, same result).
-        _scratch, xp, rscale = _cast_scratch(route[1], M, dev)
-        rs_fn = lib.g16_rowscale_pack_f32 if f32in else lib.g16_rowscale_pack_f16
-        _clib.check(rs_fn(x2d.data_ptr(), xp, rscale, M, K, ROW_SCALE_THRESHOLD, stream), "rowscale cast")
-        fn = lib.g16_hgemm_packed_f32out if out_dtype == torch.float32 else lib.g16_hgemm_packed_f16out
-        _clib.check(fn(xp, w_t.data_ptr(), out.data_ptr(), bptr, rscale, M, N, K, stream), "GEMM")
-        return out
-
-    _scratch, x16, rscale = _cast_scratch(M * K * 2, M, dev)
-    rs_fn = lib.g16_rowscale_f32 if f32in else lib.g16_rowscale_f16
-    _clib.check(rs_fn(x2d.data_ptr(), x16, rscale, M, K, ROW_SCALE_THRESHOLD, stream), "rowscale cast")
-
-    if route[0] == "splitk":
-        # Too few output tiles to fill the GPU: split K, reduce the slices in a fixed order.
-        _, ksplit, pbytes, cbytes = route
-        bufs = split_buffers(dev, stream, pbytes, cbytes)
-        st = lib.g16_hgemm_splitk(x16, w_t.data_ptr(), out.data_ptr(), 1 if out_dtype == torch.float16 else 0, bptr,
-                                  rscale, M, N, K, ksplit, *bufs, stream)
-        _clib.check(st, "split-K GEMM")
-        return out
-    fn = lib.g16_hgemm_f32out if out_dtype == torch.float32 else lib.g16_hgemm_f16out
-    _clib.check(fn(x16, w_t.data_ptr(), out.data_ptr(), bptr, rscale, M, N, K, stream), "GEMM")
+    scratch = torch.empty(scratch_bytes, device=dev, dtype=torch.uint8)
+    bufs = split_buffers(dev, stream, ws_bytes, cnt_bytes) if kind == "splitk" else (None, 0, None, 0)
+    _clib.check(lib.g16_mm_t_gemm(x2d.data_ptr(), 1 if x2d.dtype == torch.float32 else 0, w_t.data_ptr(),
+                                  out.data_ptr(), 1 if out_dtype == torch.float16 else 0, bptr, ROW_SCALE_THRESHOLD,
+                                  M, N, K, _sm_count(dev), scratch.data_ptr(), scratch_bytes, *bufs, stream), "GEMM")
     return out
 
 

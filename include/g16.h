@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 8
+#define G16_ABI_VERSION 9
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -104,6 +104,24 @@ int g16_hgemm_packed_f32out(const uint16_t* Ap, const uint16_t* B, float* C, con
 int g16_hgemm_packed_f16out(const uint16_t* Ap, const uint16_t* B, uint16_t* C, const float* bias,
                             const float* rscale, int M, int N, int K, void* stream);
 int g16_hgemm_use_packed(int M, int N, int K, int num_cus);
+
+/* ---------------------------------------------------------------------------------------------
+ * mm_t's GEMM path (src/gtx16_fp16/ops.py:86-108) in one call: the rowscale cast of x (fp32 when
+ * x_is_f32, else fp16) into `scratch`, then the GEMM on the route this library plans for num_cus
+ * compute units -- the tile-packed route where g16_hgemm_use_packed() is 1, else split-K with
+ * ksplit = g16_hgemm_plan() when that is > 1, else the plain GEMM. The same two launches, and the
+ * same result bits, as the separate entry points; one call instead of two on a path whose small
+ * shapes are bound by host time. No counterpart kernel in the reference.
+ *   scratch: at least g16_mm_t_scratch_bytes(M, N, K, num_cus) bytes, 16-byte aligned (the fp16
+ *   cast and the row scales; it must stay allocated until the GEMM has run).
+ *   workspace / counters: as g16_hgemm_splitk needs them for that ksplit (unused otherwise, then
+ *   NULL/0 is fine). thresh: as for the rowscale entry points.
+ */
+size_t g16_mm_t_scratch_bytes(int M, int N, int K, int num_cus);
+int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, void* out, int out_is_f16,
+                  const float* bias, float thresh, int M, int N, int K, int num_cus, void* scratch,
+                  size_t scratch_bytes, void* workspace, size_t workspace_bytes, uint32_t* counters,
+                  size_t counter_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Prepacked weight for the large GEMM (no counterpart kernel in the reference; it serves

@@ -52,6 +52,12 @@ def test_argument_errors_need_no_gpu(lib):
     assert lib.g16_skinny_f32in(A, A, A + 4, None, 1, 64, 64, 1, None, 0, None, 0, None) == -2  # C alignment
     # split partials beyond a 2 GiB workspace (8 x 65536 x 1024 slices x 4 bytes) are refused
     assert lib.g16_skinny_f32in(A, A, A, None, 8, 65536, 8192, 1024, A, 1 << 40, A, 1 << 20, None) == -5
+    need = lib.g16_mm_t_scratch_bytes(64, 64, 64, 256)
+    assert need == 64 * 64 * 2 + 64 * 4                                        # cast + row scales
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A, need - 1, None, 0, None, 0, None) == -4
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A + 8, need, None, 0, None, 0, None) == -2
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 64, 256, A, need, None, 0, None, 0, None) == -1
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 64, 256, A, need, None, 0, None, 0, None) == 0
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, 1000.0, None) == -1               # threshold not 2^k
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, -1024.0, None) == -1
 

@@ -490,3 +490,48 @@ def test_skinny_partial_block_ignores_rows_past_the_slice(lib, cuda, M):
     ref = oracle.skinny(_np(x), _np(w), None, "float32")
     assert np.isfinite(y[:, finite]).all()
     assert oracle.rel_err(y[:, finite], ref[:, finite]) <= SKINNY_TOL
+
+
+# One shape per route of the GEMM path: plain 128x128 tiles, split-K, tile-packed 256x256, tile-packed
+# 256x128 (128 tiles of 256^2 would leave half the CUs idle)
+@pytest.mark.parametrize("M,K,N", [(300, 136, 264), (64, 1024, 1024), (4100, 264, 2056), (2048, 264, 4096)])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_mm_t_one_call_equals_separate_launches(lib, g, cuda, M, K, N, in_dtype, out_dtype):
+    # mm_t runs g16_mm_t_gemm; the same rowscale cast and GEMM launched one by one must give the
+    # same bits
+    # outlier rows stay finite in the input dtype (fp16 tops out at 65504)
+    hi = 2e5 if out_dtype == torch.float32 and in_dtype == torch.float32 else 1e4
+    x = outlier_rows(randn((M, K), seed=0), 0.01, 2e3, hi, seed=3).to(in_dtype).to(cuda)
+    w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
+    bias = randn((N,), seed=2, scale=0.02).to(cuda)
+    y = g.mm_t(x, w, bias, out_dtype)
+    st = _stream(cuda)
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    f32in, f16out = in_dtype == torch.float32, out_dtype == torch.float16
+    s = torch.empty(M, dtype=torch.float32, device=cuda)
+    ref = torch.empty(M, N, dtype=out_dtype, device=cuda)
+    if lib.g16_hgemm_use_packed(M, N, K, cus):
+        yp = torch.empty(lib.g16_packed_a_bytes(M, K) // 2, dtype=torch.float16, device=cuda)
+        rs = lib.g16_rowscale_pack_f32 if f32in else lib.g16_rowscale_pack_f16
+        assert rs(x.data_ptr(), yp.data_ptr(), s.data_ptr(), M, K, 1024.0, st) == 0
+        fn = lib.g16_hgemm_packed_f16out if f16out else lib.g16_hgemm_packed_f32out
+        assert fn(yp.data_ptr(), w.data_ptr(), ref.data_ptr(), bias.data_ptr(), s.data_ptr(), M, N, K, st) == 0
+    else:
+        y16 = torch.empty(M, K, dtype=torch.float16, device=cuda)
+        rs = lib.g16_rowscale_f32 if f32in else lib.g16_rowscale_f16
+        assert rs(x.data_ptr(), y16.data_ptr(), s.data_ptr(), M, K, 1024.0, st) == 0
+        ks = lib.g16_hgemm_plan(M, N, K, cus)
+        if ks > 1:
+            ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ks),
+                                  lib.g16_hgemm_splitk_counter_bytes(M, N, K, ks), cuda)
+            assert lib.g16_hgemm_splitk(y16.data_ptr(), w.data_ptr(), ref.data_ptr(), 1 if f16out else 0,
+                                        bias.data_ptr(), s.data_ptr(), M, N, K, ks, ws.data_ptr(), ws.numel(),
+                                        cnt.data_ptr(), cnt.numel(), st) == 0
+        else:
+            fn = lib.g16_hgemm_f16out if f16out else lib.g16_hgemm_f32out
+            assert fn(y16.data_ptr(), w.data_ptr(), ref.data_ptr(), bias.data_ptr(), s.data_ptr(), M, N, K, st) == 0
+    torch.cuda.synchronize()
+    bits = torch.int32 if out_dtype == torch.float32 else torch.int16
+    assert torch.isfinite(y).all()
+    assert torch.equal(y.view(bits), ref.view(bits))
