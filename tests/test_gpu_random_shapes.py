@@ -22,9 +22,12 @@ def _cases(n: int = 40):
         K = int(rng.integers(1, 160)) * 8
         N = int(rng.integers(1, 130)) * 8
         out.append((i, M, K, N, bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), bool(rng.integers(0, 2))))
-    # shapes that reach the split-K and tile-packed routes
+    # shapes that reach the split-K and tile-packed routes (104 and 106: 256x128 tiles, as 128 tiles
+    # of 256x256 would leave half the CUs idle; 105: a 2-way split of 128x128 tiles)
     out += [(100, 64, 2048, 512, True, True, False), (101, 1100, 264, 4096, False, True, True),
-            (102, 2300, 136, 2048, True, False, True), (103, 33, 4096, 256, False, False, False)]
+            (102, 2300, 136, 2048, True, False, True), (103, 33, 4096, 256, False, False, False),
+            (104, 2048, 136, 4096, False, False, True), (105, 512, 2048, 2048, True, True, True),
+            (106, 1900, 264, 3896, True, False, False)]
     return out
 
 
