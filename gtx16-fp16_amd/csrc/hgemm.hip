@@ -208,10 +208,15 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   };
   auto rsrc_b = [&](int k0) {
     if constexpr (PACKED_B) {
-      static_assert(PACKED_A && Cfg::BN == 256, "a packed weight pairs with packed activations on the 256 tile");
+      // The packed weight holds B^T in 256-row blocks (g16_pack_weight). A 256-column tile streams
+      // whole 16 KB blocks; a 128-column tile streams one half of each: rows 0-127 of a block are
+      // its first 8 KB (chunks q < 8), rows 128-255 the second, each already the 128-row stage
+      // image (the row swizzle repeats every 8 rows). Step k0 adds k0/BK blocks (16 KB) either way.
+      static_assert(PACKED_A && (Cfg::BN == 256 || Cfg::BN == 128), "packed weight: the 256-row tiles");
+      constexpr int kHalves = 256 / Cfg::BN;
       return __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<_Float16*>(B) + static_cast<size_t>(tn) * ceil_div(K, BK) * (Cfg::B_BYTES / 2), 0, 0x7fffffff,
-          kRawBufferDword3);
+          const_cast<_Float16*>(B) + static_cast<size_t>(tn / kHalves) * ceil_div(K, BK) * 8192 + (tn % kHalves) * 4096, 0,
+          0x7fffffff, kRawBufferDword3);
     } else {
       return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B) + static_cast<size_t>(k0) * N + n0, 0,
                                                0x7fffffff, kRawBufferDword3);
@@ -645,7 +650,8 @@ using GemmFn = void (*)(const _Float16*, const _Float16*, void*, const float*, c
 
 template <bool OUT_F16>
 GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b) {
-  if (packed_b) return hgemm_kernel<Cfg256, OUT_F16, false, true, true>;
+  if (packed_b)
+    return t == Tile::T256N ? hgemm_kernel<Cfg256n, OUT_F16, false, true, true> : hgemm_kernel<Cfg256, OUT_F16, false, true, true>;
   if (packed) return t == Tile::T256N ? hgemm_kernel<Cfg256n, OUT_F16, false, true> : hgemm_kernel<Cfg256, OUT_F16, false, true>;
   if (splitk) {
     switch (t) {
@@ -687,9 +693,9 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   const KSplit ks = ksplit_for(K, ksplit);
   Plan p = choose_tile(M, N, ks.ksplit > 1, device_cus());
   if (packed) {
-    // the packed A layout is the stage image of the 256-row tiles: the 256x256 tile, or the
-    // 256x128 one where the plan picks it; a packed weight pairs with the 256x256 tile only
-    if (packed_b || p.tile != Tile::T256N) p = Plan{Tile::T256, 256, 256, ceil_div(M, 256), ceil_div(N, 256)};
+    // the packed layouts are the stage images of the 256-row tiles: the 256x256 tile, or the
+    // 256x128 one where the plan picks it
+    if (p.tile != Tile::T256N) p = Plan{Tile::T256, 256, 256, ceil_div(M, 256), ceil_div(N, 256)};
   }
   float* part = nullptr;
   uint32_t* counters = nullptr;
@@ -780,9 +786,9 @@ extern "C" int g16_hgemm_use_packed(int M, int N, int K, int num_cus) {
 }
 
 extern "C" int g16_hgemm_use_packed_b(int M, int N, int K, int num_cus) {
-  // A prepacked weight (g16_pack_weight) is the 256x256 tile's B stage image: it serves the packed
-  // route where that route runs the 256x256 tile.
-  return g16_hgemm_use_packed(M, N, K, num_cus) && g16::choose_tile(M, N, false, num_cus).tile == g16::Tile::T256 ? 1 : 0;
+  // A prepacked weight (g16_pack_weight) holds the B stage images of both 256-row tiles (whole
+  // blocks for 256 columns, half blocks for 128), so it serves the whole packed route.
+  return g16_hgemm_use_packed(M, N, K, num_cus);
 }
 
 extern "C" int g16_hgemm_packed_f32out(const uint16_t* Ap, const uint16_t* B, float* C, const float* bias,

@@ -127,10 +127,10 @@ int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, void* out, i
  * Prepacked weight for the large GEMM (no counterpart kernel in the reference; it serves
  * FastLinear, src/gtx16_fp16/linear.py:12-76, whose fp16 weight_t [K,N] is fixed after from_linear,
  * linear.py:30-37). g16_pack_weight writes w_t transposed ([N,K]) in the tile-packed layout above
- * (rows = N); g16_hgemm_packed_ab_* is the 256x256 GEMM with both operands packed. Same values and
+ * (rows = N); g16_hgemm_packed_ab_* is the packed GEMM with both operands packed. Same values and
  * the same result bits as g16_hgemm_packed_* on the unpacked weight.
- * g16_hgemm_use_packed_b() is 1 where the packed route runs the 256x256 tile, the one a packed
- * weight serves (elsewhere the packed route runs the 256x128 tile on the unpacked weight).
+ * g16_hgemm_use_packed_b() is 1 where a packed weight serves mm_t's route: the packed route, on
+ * either 256-row tile (the 256x128 tile streams half blocks of the same layout).
  */
 size_t g16_packed_b_bytes(int K, int N);
 int g16_pack_weight(const uint16_t* w_t, uint16_t* wp, int K, int N, void* stream);

@@ -75,12 +75,12 @@ def test_plans_and_buffer_sizes(lib):
     # tiles that leave CUs idle split as far as one workgroup per CU allows
     assert lib.g16_hgemm_plan(512, 4096, 4096, 256) == 2             # 128 tiles of 128x128
     assert lib.g16_hgemm_plan(768, 4096, 4096, 256) == 1             # 192 tiles: 2 slices would overflow
-    # 128 tiles of 256x256 would leave half the CUs idle: 256 tiles of 256x128 instead, packed A,
-    # no split; a prepacked weight serves only the 256x256 tile
+    # 128 tiles of 256x256 would leave half the CUs idle: 256 tiles of 256x128 instead, packed A
+    # (and a packed weight, whose blocks the 128-column tiles read by halves), no split
     assert lib.g16_hgemm_plan(2048, 4096, 4096, 256) == 1
     assert lib.g16_hgemm_plan(2048, 4096, 8192, 256) == 1
     assert lib.g16_hgemm_use_packed(2048, 4096, 4096, 256) == 1
-    assert lib.g16_hgemm_use_packed_b(2048, 4096, 4096, 256) == 0
+    assert lib.g16_hgemm_use_packed_b(2048, 4096, 4096, 256) == 1
     assert lib.g16_hgemm_use_packed_b(4096, 4096, 4096, 256) == 1
     assert lib.g16_hgemm_use_packed_b(1536, 4096, 4096, 256) == 0    # 128x128 tiles, not packed
     # skinny: whole 16-row blocks per wavefront, at most one workgroup per CU

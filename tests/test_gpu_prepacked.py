@@ -15,7 +15,9 @@ from _packing import pack_a
 pytestmark = pytest.mark.gpu
 
 # shapes on the tile-packed 256x256 route (ragged M, K and N included)
-ROUTE_SHAPES = [(4096, 4096, 4096), (2300, 264, 4096), (4100, 1000, 2056)]
+# the last two run 256x128 tiles (128 tiles of 256x256 would leave half the CUs idle), which read the
+# packed weight by half blocks; (1800, 136, 3896) also has a ragged last half block
+ROUTE_SHAPES = [(4096, 4096, 4096), (2300, 264, 4096), (4100, 1000, 2056), (2048, 264, 4096), (1800, 136, 3896)]
 
 
 @pytest.fixture(scope="module")
