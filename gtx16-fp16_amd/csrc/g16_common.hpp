@@ -26,12 +26,36 @@ struct identity {
   using type = T;
 };
 
-// Launch `kern` with hipLaunchKernel so the launch status comes back as a value (a positive
-// hipError_t), not through the sticky per-thread error state.
+// Makes the device that owns `stream` current until the end of the scope, when it is not the
+// current one already (a caller on a multi-GPU host may pass a stream of another device than the
+// thread's current one, e.g. a layer placed on GPU 1 called while GPU 0 is current): the kernel
+// then runs where the stream and its buffers are. The null stream belongs to the current device.
+class StreamDeviceScope {
+ public:
+  explicit StreamDeviceScope(hipStream_t stream) {
+    int sd = 0, cur = 0;
+    if (stream == nullptr || hipStreamGetDevice(stream, &sd) != hipSuccess || hipGetDevice(&cur) != hipSuccess ||
+        sd == cur)
+      return;
+    if (hipSetDevice(sd) == hipSuccess) prev_ = cur;
+  }
+  ~StreamDeviceScope() {
+    if (prev_ >= 0) (void)hipSetDevice(prev_);
+  }
+  StreamDeviceScope(const StreamDeviceScope&) = delete;
+  StreamDeviceScope& operator=(const StreamDeviceScope&) = delete;
+
+ private:
+  int prev_ = -1;
+};
+
+// Launch `kern` with hipLaunchKernel on `stream`'s device, so the launch status comes back as a
+// value (a positive hipError_t), not through the sticky per-thread error state.
 template <typename... KArgs>
 static inline int launch(void (*kern)(KArgs...), dim3 grid, dim3 block, hipStream_t stream,
                          typename identity<KArgs>::type... args) {
   void* argv[] = {static_cast<void*>(&args)...};
+  StreamDeviceScope on_stream_device(stream);
   hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(kern), grid, block, argv, 0, stream);
   return static_cast<int>(err);
 }

@@ -9,8 +9,11 @@
  * Conventions shared by every entry point:
  *   - Plain device pointers and sizes; no torch types. fp16 data is passed as uint16_t bit
  *     patterns (IEEE binary16), fp32 as float.
- *   - The call enqueues work on `stream` (a hipStream_t; NULL = the legacy default stream) and
- *     returns at once. It never synchronises and never allocates or frees device memory.
+ *   - The call enqueues work on `stream` (a hipStream_t; NULL = the legacy default stream of the
+ *     current device) and returns at once. The kernels run on the device that owns `stream`: when
+ *     that is not the calling thread's current device, the call makes it current for the launch
+ *     and restores the previous one. It never synchronises and never allocates or frees device
+ *     memory.
  *   - Return value: 0 on success; a negative G16_E* code for an argument the library rejects
  *     (nothing is enqueued then); a positive hipError_t if the HIP launch itself fails.
  *     g16_strerror() names both kinds.
