@@ -2,7 +2,8 @@
 
     python gtx16-fp16_amd/build_lib.py [--jobs N] [--verbose]
 
-Compiles every ``csrc/*.hip`` for gfx950 only and links ``gtx16_fp16/_lib/libg16.so``. The library
+Compiles every ``csrc/*.hip`` for gfx950 only and links ``gtx16_fp16/_lib/libg16.so``; then builds
+``csrc/fastcall.c`` (host C, with gcc) into the CPython extension ``gtx16_fp16/_lib/_g16fast``. The library
 lists ``libamdhip64.so.7`` as a dependency by SONAME; torch-ROCm ships a runtime with the same
 SONAME, so when ``torch`` is imported first (as ``gtx16_fp16`` does) the library binds to the
 runtime torch already loaded and shares its device context and streams.
@@ -15,6 +16,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
@@ -73,7 +75,21 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
+    build_fastcall(verbose)
     return LIB
+
+
+def build_fastcall(verbose: bool = False) -> Path:
+    """Compile the CPython extension _g16fast (host C only, no device code) next to libg16.so."""
+    out = OUT_DIR / ("_g16fast" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no C compiler (gcc) for the _g16fast extension")
+    _run([cc, "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-cast-function-type",
+          f"-I{sysconfig.get_paths()['include']}", str(CSRC / "fastcall.c"), "-o", str(tmp)], verbose)
+    os.replace(tmp, out)
+    return out
 
 
 def main(argv: list[str] | None = None) -> int:

@@ -8,6 +8,8 @@ fallback implementation behind this module.
 from __future__ import annotations
 
 import ctypes
+import importlib.util
+import sysconfig
 import threading
 from pathlib import Path
 
@@ -85,6 +87,34 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+_fast = None
+
+
+def fast():
+    """The CPython extension ``_g16fast`` (built next to the library from ``csrc/fastcall.c``), bound
+    to the loaded library: ``skinny_f32in`` and ``mm_t_gemm`` take the same arguments as the C
+    entry points (pointers as ints or None) and return their status, with argument conversion
+    that costs a few ns per argument instead of ctypes' ~0.1 us. Missing -> ``RuntimeError``."""
+    global _fast
+    if _fast is not None:
+        return _fast
+    lib = load()
+    with _lock:
+        if _fast is None:
+            p = LIB_PATH.parent / ("_g16fast" + sysconfig.get_config_var("EXT_SUFFIX"))
+            if not p.exists():
+                raise RuntimeError(
+                    f"gtx16_fp16: extension {p} is missing; build it with "
+                    "`python gtx16-fp16_amd/build_lib.py` (or __graft_entry__.build())")
+            spec = importlib.util.spec_from_file_location("_g16fast", p)
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            mod.bind(ctypes.cast(lib.g16_skinny_f32in, ctypes.c_void_p).value,
+                     ctypes.cast(lib.g16_mm_t_gemm, ctypes.c_void_p).value)
+            _fast = mod
+    return _fast
 
 
 def strerror(status: int) -> str:

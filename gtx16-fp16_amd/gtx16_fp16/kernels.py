@@ -58,7 +58,7 @@ def launch(kernel, args: list, what: str = "g16 kernel") -> None:
 
 
 class PreparedLaunch:
-    """A bound entry point whose per-call Python work is only the ctypes call itself: for the
+    """A bound entry point whose per-call Python work is only the call itself: for the
     token-by-token FastLinear path (kernels.py:324-338)."""
 
     __slots__ = ("fn", "what")

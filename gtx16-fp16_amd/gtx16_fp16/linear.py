@@ -76,7 +76,7 @@ class FastLinear(nn.Module):
             if ok:
                 lib = _clib.load()
                 ksplit = lib.g16_skinny_plan(M, N, K, _sm_count(dev))
-                pl = PreparedLaunch(lib.g16_skinny_f32in, "skinny GEMM")
+                pl = PreparedLaunch(_clib.fast().skinny_f32in, "skinny GEMM")
                 sizes = (lib.g16_skinny_workspace_bytes(M, N, K, ksplit), lib.g16_skinny_counter_bytes(M, N, K, ksplit))
             entry = (pl, ksplit, sizes, w.data_ptr(), bptr)
             self._skinny[key] = entry

@@ -177,7 +177,7 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
             _remember(key, plan)
         ksplit = plan[0]
         bufs = split_buffers(dev, stream, plan[1], plan[2])
-        fn = lib.g16_skinny_f32in if x2d.dtype == torch.float32 else lib.g16_skinny_f16in
+        fn = _clib.fast().skinny_f32in if x2d.dtype == torch.float32 else lib.g16_skinny_f16in
         _clib.check(fn(x2d.data_ptr(), w_t.data_ptr(), out.data_ptr(), bptr, M, N, K, ksplit, *bufs, stream),
                     "skinny GEMM")
         return out if out_dtype == torch.float32 else out.to(out_dtype)
@@ -190,7 +190,7 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
     scratch = torch.empty(scratch_bytes, device=dev, dtype=torch.uint8)
     bufs = split_buffers(dev, stream, ws_bytes, cnt_bytes) if kind == "splitk" else (None, 0, None, 0)
-    _clib.check(lib.g16_mm_t_gemm(x2d.data_ptr(), 1 if x2d.dtype == torch.float32 else 0, w_t.data_ptr(),
+    _clib.check(_clib.fast().mm_t_gemm(x2d.data_ptr(), 1 if x2d.dtype == torch.float32 else 0, w_t.data_ptr(),
                                   out.data_ptr(), 1 if out_dtype == torch.float16 else 0, bptr, ROW_SCALE_THRESHOLD,
                                   M, N, K, _sm_count(dev), scratch.data_ptr(), scratch_bytes, *bufs, stream), "GEMM")
     return out

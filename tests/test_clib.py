@@ -95,6 +95,28 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_hgemm_splitk_counter_bytes(64, 1024, 1024, 4) > 0
 
 
+def test_fast_extension_matches_the_c_entry_points(lib):
+    # _g16fast forwards its arguments unchanged: the same rejected calls give the same statuses
+    fast = _clib.fast()
+    A = 0x1000
+    assert fast.skinny_f32in(A, A, A, None, 9, 64, 64, 1, None, 0, None, 0, None) == -1
+    assert fast.skinny_f32in(A, A, A + 4, None, 1, 64, 64, 1, None, 0, None, 0, None) == -2
+    assert fast.skinny_f32in(A, A, A, None, 4, 4096, 4096, 8, A, 1 << 30, None, 0, None) == -4
+    assert fast.skinny_f32in(A, A, A, None, 8, 65536, 8192, 1024, A, 1 << 40, A, 1 << 20, None) == -5
+    need = lib.g16_mm_t_scratch_bytes(64, 64, 64, 256)
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A, need - 1, None, 0, None, 0, None) == -4
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A + 8, need, None, 0, None, 0, None) == -2
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 64, 256, A, need, None, 0, None, 0, None) == -1
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1000.0, 64, 64, 64, 256, A, need, None, 0, None, 0, None) == -1
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 64, 256, A, need, None, 0, None, 0, None) == 0
+    with pytest.raises(TypeError):
+        fast.skinny_f32in(A, A, A)
+    with pytest.raises(OverflowError):
+        fast.skinny_f32in(A, A, A, None, 1 << 40, 64, 64, 1, None, 0, None, 0, None)
+    with pytest.raises(TypeError):
+        fast.mm_t_gemm(A, 1, A, A, 0, None, "x", 64, 64, 64, 256, A, need, None, 0, None, 0, None)
+
+
 def test_nonzero_status_raises_runtime_error():
     # kernels.py:299-302 convention: a failed launch raises RuntimeError naming the status
     with pytest.raises(RuntimeError, match="status 98"):
