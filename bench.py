@@ -223,7 +223,7 @@ def bench_skinny(torch, lib, g, steps: int, warmup: int, dev, copies: int = 16) 
     }
 
 
-def _time_call(torch, fn, steps: int, warmup: int = 3) -> float:
+def _time_call(torch, fn, steps: int, warmup: int = 20) -> float:
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
