@@ -613,8 +613,14 @@ int device_cus() {
 // outputs take the 256x256 tile once it gives more than half the CUs a workgroup; just below that
 // (3/8 to 1/2 of the CUs), the 256x128 tile on the same schedule fills them instead (2048 x 4096^2,
 // 128 tiles of 256^2 on 256 CUs: 89 us, 256 tiles of 256x128: 76-82 us; with 144 tiles of 256^2
-// the 256x128 grid would overflow the CUs: 93 vs 128 us).
-Plan choose_tile(int M, int N, bool /*splitk*/, int num_cus) {
+// the 256x128 grid would overflow the CUs: 93 vs 128 us). Below that, with K <= 2048, the
+// 4-wavefront tile with the most tiles that still fit one round on the CUs (32x128, then 64x128,
+// else 128x128): a small GEMM is bound by how many CUs it occupies (graph-timed, 256 CUs: 1024^3
+// 13.7 us on 128^2 tiles, 10.3 on 64x128, 8.9 on 32x128; 768 x 1024^2 13.4 -> 8.6; 512 x 1024 x
+// 3072 14.5 -> 11.2 on 64x128, where 32x128 tiles would need 1.5 rounds; 1024 x 768 x 3072 stays
+// on 128^2, 14.4 against 16.1-17.5). With longer K the 128^2 tile and a split win (256 x 4096^2:
+// 21.3 us split 4 ways, 23.5 on unsplit 32x128 tiles).
+Plan choose_tile(int M, int N, int K, int num_cus) {
   Plan p{};
   const long t256 = static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256);
   if (M <= 32) {
@@ -625,6 +631,10 @@ Plan choose_tile(int M, int N, bool /*splitk*/, int num_cus) {
     p.tile = Tile::T256; p.bm = 256; p.bn = 256;
   } else if (M >= 1024 && N >= 256 && 8 * t256 > 3 * num_cus) {
     p.tile = Tile::T256N; p.bm = 256; p.bn = 128;
+  } else if (K <= 2048 && static_cast<long>(ceil_div(M, 32)) * ceil_div(N, 128) <= num_cus) {
+    p.tile = Tile::T32; p.bm = 32; p.bn = 128;
+  } else if (K <= 2048 && static_cast<long>(ceil_div(M, 64)) * ceil_div(N, 128) <= num_cus) {
+    p.tile = Tile::T64; p.bm = 64; p.bn = 128;
   } else {
     p.tile = Tile::T128; p.bm = 128; p.bn = 128;
   }
@@ -691,7 +701,7 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return G16_E_NULL;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return G16_E_ALIGN;
   const KSplit ks = ksplit_for(K, ksplit);
-  Plan p = choose_tile(M, N, ks.ksplit > 1, device_cus());
+  Plan p = choose_tile(M, N, K, device_cus());
   if (packed) {
     // the packed layouts are the stage images of the 256-row tiles: the 256x256 tile, or the
     // 256x128 one where the plan picks it
@@ -728,12 +738,9 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   // that runs a second round; 768 x 4096^2: 192 tiles unsplit 48 us, 2 slices 54 us;
   // 512 x 4096^2: 128 tiles unsplit 44 us, 2 slices 36 us; 512 x 11008 x 4096: 104 vs 75 us).
   if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0) return 1;
-  const g16::Plan p = g16::choose_tile(M, N, false, num_cus);
-  const int tiles = p.ntm * p.ntn;
+  const g16::Plan q = g16::choose_tile(M, N, K, num_cus);
+  const int tiles = q.ntm * q.ntn;
   if (tiles >= num_cus || K < 512) return 1;
-  const g16::Plan q = g16::choose_tile(M, N, true, num_cus);
-  const int qtiles = q.ntm * q.ntn;
-  if (qtiles != tiles) return 1;
   // At most 8 slices: the last slice to arrive reads every other slice's fp32 tile at one CU's
   // bandwidth, so beyond ~8 the reduction costs more than the extra parallelism gains (measured:
   // 64x4096x1024 12.1 us at 8 vs 14.3 us at 16). Each slice keeps >= 256 K (>= 1024 K for the
@@ -757,14 +764,14 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
 extern "C" size_t g16_hgemm_splitk_workspace_bytes(int M, int N, int K, int ksplit) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const g16::KSplit ks = g16::ksplit_for(K, ksplit);
-  const g16::Plan p = g16::choose_tile(M, N, ks.ksplit > 1, g16::device_cus());
+  const g16::Plan p = g16::choose_tile(M, N, K, g16::device_cus());
   return g16::splitk_ws_bytes(p, ks.ksplit);
 }
 
 extern "C" size_t g16_hgemm_splitk_counter_bytes(int M, int N, int K, int ksplit) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const g16::KSplit ks = g16::ksplit_for(K, ksplit);
-  const g16::Plan p = g16::choose_tile(M, N, ks.ksplit > 1, g16::device_cus());
+  const g16::Plan p = g16::choose_tile(M, N, K, g16::device_cus());
   return g16::splitk_counter_bytes(p, ks.ksplit);
 }
 
@@ -781,7 +788,7 @@ extern "C" int g16_hgemm_f16out(const uint16_t* A, const uint16_t* B, uint16_t* 
 extern "C" int g16_hgemm_use_packed(int M, int N, int K, int num_cus) {
   // The packed route pays off where the plain plan already picks the 256x256 tile without a split.
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  const g16::Tile t = g16::choose_tile(M, N, false, num_cus).tile;
+  const g16::Tile t = g16::choose_tile(M, N, K, num_cus).tile;
   return (t == g16::Tile::T256 || t == g16::Tile::T256N) && g16_hgemm_plan(M, N, K, num_cus) == 1 ? 1 : 0;
 }
 

@@ -67,9 +67,10 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_hgemm_plan(4096, 4096, 4096, 256) == 1           # enough tiles: no split
     assert lib.g16_hgemm_plan(64, 1024, 4096, 256) > 1              # few tiles: split K
     # measured-best splits: >= 1024 K per slice on the 128x128 tile, >= 256 K on the 64x128 tile
-    assert lib.g16_hgemm_plan(1024, 1024, 1024, 256) == 1
-    assert lib.g16_hgemm_plan(1024, 1024, 2048, 256) == 2
-    assert lib.g16_hgemm_plan(512, 512, 512, 256) == 1
+    assert lib.g16_hgemm_plan(1024, 1024, 1024, 256) == 1            # 256 tiles of 32x128
+    assert lib.g16_hgemm_plan(1024, 1024, 2048, 256) == 1
+    assert lib.g16_hgemm_plan(512, 1024, 1024, 256) == 2             # 128 tiles of 32x128
+    assert lib.g16_hgemm_plan(512, 512, 512, 256) == 2               # 64 tiles of 32x128, >= 256 K a slice
     assert lib.g16_hgemm_plan(64, 1024, 1024, 256) == 4
     assert lib.g16_hgemm_plan(64, 1024, 4096, 256) == 8
     # tiles that leave CUs idle split as far as one workgroup per CU allows

@@ -20,7 +20,7 @@ def _ceil(a: int, b: int) -> int:
     return -(-a // b)
 
 
-def _tiles(M: int, N: int, num_cus: int) -> int:
+def _tiles(M: int, N: int, K: int, num_cus: int) -> int:
     # the library's tile choice (choose_tile): 32x128, 64x128, 256x256, 256x128 or 128x128
     if M <= 64:
         return _ceil(N, 128)
@@ -29,6 +29,9 @@ def _tiles(M: int, N: int, num_cus: int) -> int:
         return t256
     if M >= 1024 and N >= 256 and 8 * t256 > 3 * num_cus:
         return _ceil(M, 256) * _ceil(N, 128)
+    for bm in (32, 64):  # short K: the smallest 4-wavefront tile whose grid fits one round
+        if K <= 2048 and _ceil(M, bm) * _ceil(N, 128) <= num_cus:
+            return _ceil(M, bm) * _ceil(N, 128)
     return _ceil(M, 128) * _ceil(N, 128)
 
 
@@ -40,7 +43,7 @@ cus = st.sampled_from([64, 120, 256, 304])
 @given(M=st.integers(min_value=9, max_value=70000), N=dims, K=dims, num_cus=cus)
 def test_gemm_plan_limits(lib, M, N, K, num_cus):
     ks = lib.g16_hgemm_plan(M, N, K, num_cus)
-    tiles = _tiles(M, N, num_cus)
+    tiles = _tiles(M, N, K, num_cus)
     assert 1 <= ks <= 8
     if ks > 1:
         # split only when tiles leave CUs idle, never past one workgroup per CU, >= 256 K a slice
