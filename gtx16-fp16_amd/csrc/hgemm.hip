@@ -613,13 +613,14 @@ int device_cus() {
 // outputs take the 256x256 tile once it gives more than half the CUs a workgroup; just below that
 // (3/8 to 1/2 of the CUs), the 256x128 tile on the same schedule fills them instead (2048 x 4096^2,
 // 128 tiles of 256^2 on 256 CUs: 89 us, 256 tiles of 256x128: 76-82 us; with 144 tiles of 256^2
-// the 256x128 grid would overflow the CUs: 93 vs 128 us). Below that, with K <= 2048, the
+// the 256x128 grid would overflow the CUs: 93 vs 128 us). Below that, with K <= 3072, the
 // 4-wavefront tile with the most tiles that still fit one round on the CUs (32x128, then 64x128,
-// else 128x128): a small GEMM is bound by how many CUs it occupies (graph-timed, 256 CUs: 1024^3
-// 13.7 us on 128^2 tiles, 10.3 on 64x128, 8.9 on 32x128; 768 x 1024^2 13.4 -> 8.6; 512 x 1024 x
-// 3072 14.5 -> 11.2 on 64x128, where 32x128 tiles would need 1.5 rounds; 1024 x 768 x 3072 stays
-// on 128^2, 14.4 against 16.1-17.5). With longer K the 128^2 tile and a split win (256 x 4096^2:
-// 21.3 us split 4 ways, 23.5 on unsplit 32x128 tiles).
+// else 128x128): a small GEMM is bound by how many CUs it occupies (graph-timed, 256 CUs, M x N x K:
+// 1024^3 13.7 us on 128^2 tiles, 10.3 on 64x128, 8.9 on 32x128; 768 x 1024^2 13.4 -> 8.6;
+// 512 x 3072 x 1024 14.5 -> 11.2 on 64x128, where 32x128 tiles would need 1.5 rounds;
+// 1024 x 3072 x 768 stays on 128^2, 14.4 against 16.1-17.5; 256 x 1024 x 3072 16-19 -> 9.6 split
+// 4 ways; 1024 x 1024 x 3072 22 -> 19). At K = 4096 the 128^2 tile with a split wins or ties
+// (512 x 4096^2 30.0 us against 31.2 on 64x128 and 37.3 on 32x128).
 Plan choose_tile(int M, int N, int K, int num_cus) {
   Plan p{};
   const long t256 = static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256);
@@ -631,9 +632,9 @@ Plan choose_tile(int M, int N, int K, int num_cus) {
     p.tile = Tile::T256; p.bm = 256; p.bn = 256;
   } else if (M >= 1024 && N >= 256 && 8 * t256 > 3 * num_cus) {
     p.tile = Tile::T256N; p.bm = 256; p.bn = 128;
-  } else if (K <= 2048 && static_cast<long>(ceil_div(M, 32)) * ceil_div(N, 128) <= num_cus) {
+  } else if (K <= 3072 && static_cast<long>(ceil_div(M, 32)) * ceil_div(N, 128) <= num_cus) {
     p.tile = Tile::T32; p.bm = 32; p.bn = 128;
-  } else if (K <= 2048 && static_cast<long>(ceil_div(M, 64)) * ceil_div(N, 128) <= num_cus) {
+  } else if (K <= 3072 && static_cast<long>(ceil_div(M, 64)) * ceil_div(N, 128) <= num_cus) {
     p.tile = Tile::T64; p.bm = 64; p.bn = 128;
   } else {
     p.tile = Tile::T128; p.bm = 128; p.bn = 128;

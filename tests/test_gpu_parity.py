@@ -134,6 +134,24 @@ SHAPES = [  # (M, K, N) -- reference sweep, tests/test_correctness.py:14-18
 ]
 
 
+# Medium shapes with K <= 3072 run on the 32x128 or 64x128 tile whose grid fills one round of the
+# CUs (unsplit, or split where the tiles still leave CUs idle); bitwise repeatable either way.
+@pytest.mark.parametrize("M,K,N", [(256, 3072, 1024), (1024, 3072, 1024), (520, 2056, 3072), (1024, 1024, 1024)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_short_k_small_tiles_match_oracle(g, cuda, M, K, N, out_dtype):
+    x = randn((M, K), seed=M + 5 * K, scale=0.5)
+    w = randn((K, N), seed=N + 3 * K, scale=0.5, dtype=torch.float16)
+    b = randn((N,), seed=N + 1)
+    xd, wd, bd = x.to(cuda), w.to(cuda), b.to(cuda)
+    y = g.mm_t(xd, wd, bd, out_dtype)
+    y2 = g.mm_t(xd, wd, bd, out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16) if out_dtype == torch.float16 else y.view(torch.int32),
+                       y2.view(torch.int16) if out_dtype == torch.float16 else y2.view(torch.int32))
+    ref = oracle.mm_t(_np(x), _np(w), _np(b), "float32")
+    assert oracle.rel_err(_np(y.float()), ref) <= GEMM_TOL
+
+
 @pytest.mark.parametrize("M,K,N", SHAPES)
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 @pytest.mark.parametrize("with_bias", [False, True])

@@ -30,7 +30,7 @@ def _tiles(M: int, N: int, K: int, num_cus: int) -> int:
     if M >= 1024 and N >= 256 and 8 * t256 > 3 * num_cus:
         return _ceil(M, 256) * _ceil(N, 128)
     for bm in (32, 64):  # short K: the smallest 4-wavefront tile whose grid fits one round
-        if K <= 2048 and _ceil(M, bm) * _ceil(N, 128) <= num_cus:
+        if K <= 3072 and _ceil(M, bm) * _ceil(N, 128) <= num_cus:
             return _ceil(M, bm) * _ceil(N, 128)
     return _ceil(M, 128) * _ceil(N, 128)
 
