@@ -624,7 +624,11 @@ int device_cus() {
 Plan choose_tile(int M, int N, int K, int num_cus) {
   Plan p{};
   const long t256 = static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256);
-  if (M <= 32) {
+  if (M <= 32 || (M <= 64 && 4L * ceil_div(N, 128) <= num_cus)) {
+    // M = 33..64 on two rows of 32x128 tiles while they fill at most half the CUs, so the split
+    // still doubles them (graph-timed, M x N x K: 64 x 1024^2 8.6 -> 6.8 us, 64 x 1024 x 4096
+    // 11.4 -> 9.7, 64 x 4096^2 13.9 -> 11.9, 64 x 4096 x 11008 23.6 -> 21.5); with more tiles than
+    // that, 64x128 tiles split twice beat unsplit 32x128 ones (64 x 11008 x 4096: 21.4 vs 31.3 us).
     p.tile = Tile::T32; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
     p.tile = Tile::T64; p.bm = 64; p.bn = 128;

@@ -22,8 +22,10 @@ def _ceil(a: int, b: int) -> int:
 
 def _tiles(M: int, N: int, K: int, num_cus: int) -> int:
     # the library's tile choice (choose_tile): 32x128, 64x128, 256x256, 256x128 or 128x128
-    if M <= 64:
+    if M <= 32:
         return _ceil(N, 128)
+    if M <= 64:  # two rows of 32x128 tiles while they fill at most half the CUs, else 64x128
+        return 2 * _ceil(N, 128) if 4 * _ceil(N, 128) <= num_cus else _ceil(N, 128)
     t256 = _ceil(M, 256) * _ceil(N, 256)
     if M >= 1024 and N >= 256 and 2 * t256 > num_cus:
         return t256
