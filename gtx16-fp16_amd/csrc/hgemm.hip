@@ -597,17 +597,40 @@ struct Plan {
   int ntm, ntn;
 };
 
-// Compute units of the current device (cached per device; 256, the MI355X count, if the query fails).
-int device_cus() {
+// Compute units of device `dev` (cached per device; 256, the MI355X count, if the query fails).
+int cus_of_device(int dev) {
   static int cache[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (dev < 0 || dev >= 64) return 256;
   if (cache[dev] == 0) {
     int n = 0;
     cache[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
   }
   return cache[dev];
 }
+
+// Compute units of the device that owns `stream` (the null stream: the current device), for the
+// entry points that take no CU count of their own.
+int stream_cus(hipStream_t stream) {
+  int dev = 0;
+  if (stream == nullptr || hipStreamGetDevice(stream, &dev) != hipSuccess) {
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+  }
+  return cus_of_device(dev);
+}
+
+// Compute units of the current device, for the size queries when the caller passes num_cus <= 0.
+int current_cus() {
+  int dev = 0;
+  return hipGetDevice(&dev) == hipSuccess ? cus_of_device(dev) : 256;
+}
+
+// Size limits of the 32-bit buffer offsets the DMA uses. A row-major A offset is at most
+// BM * K * 2 bytes past its tile row (BM <= 256), a packed A or B offset at most 16 KB per K step of
+// 32 past its tile row, and a row-major B offset at most BK * N * 2 bytes (BK <= 64) past its K
+// step; every one must stay below the descriptors' 2^31 - 1 byte range (an offset past it reads
+// zeros, which would make an oversized operand's product silently wrong).
+constexpr int kMaxK = G16_GEMM_MAX_K;
+constexpr int kMaxN = G16_GEMM_MAX_N;
 
 // The same tile with or without a split: a split only spreads K over more workgroups. Large
 // outputs take the 256x256 tile once it gives more than half the CUs a workgroup; just below that
@@ -697,16 +720,20 @@ size_t splitk_counter_bytes(const Plan& p, int ksplit) {
   return counter_bytes(static_cast<size_t>(p.ntm) * p.ntn);
 }
 
+// Launches the GEMM on the tile choose_tile() picks for num_cus compute units (<= 0: the CU count of
+// the stream's device), so that a caller who planned ksplit and sized the split buffers for a CU
+// count gets exactly that grid.
 int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, const float* bias, const float* rscale,
-                int M, int N, int K, int ksplit, void* ws, size_t ws_bytes, uint32_t* counters_in,
+                int M, int N, int K, int ksplit, int num_cus, void* ws, size_t ws_bytes, uint32_t* counters_in,
                 size_t counter_bytes_in, void* stream, bool packed = false, bool packed_b = false) {
-  if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0) return G16_E_SHAPE;
+  if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0 || K > kMaxK || N > kMaxN) return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
   if (ksplit < 1 || ksplit > 256) return G16_E_SPLIT;
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return G16_E_NULL;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return G16_E_ALIGN;
   const KSplit ks = ksplit_for(K, ksplit);
-  Plan p = choose_tile(M, N, K, device_cus());
+  if (num_cus <= 0) num_cus = stream_cus(static_cast<hipStream_t>(stream));
+  Plan p = choose_tile(M, N, K, num_cus);
   if (packed) {
     // the packed layouts are the stage images of the 256-row tiles: the 256x256 tile, or the
     // 256x128 one where the plan picks it
@@ -766,28 +793,28 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   return g16::ksplit_for(K, ks < 1 ? 1 : ks).ksplit;
 }
 
-extern "C" size_t g16_hgemm_splitk_workspace_bytes(int M, int N, int K, int ksplit) {
+extern "C" size_t g16_hgemm_splitk_workspace_bytes(int M, int N, int K, int ksplit, int num_cus) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const g16::KSplit ks = g16::ksplit_for(K, ksplit);
-  const g16::Plan p = g16::choose_tile(M, N, K, g16::device_cus());
+  const g16::Plan p = g16::choose_tile(M, N, K, num_cus > 0 ? num_cus : g16::current_cus());
   return g16::splitk_ws_bytes(p, ks.ksplit);
 }
 
-extern "C" size_t g16_hgemm_splitk_counter_bytes(int M, int N, int K, int ksplit) {
+extern "C" size_t g16_hgemm_splitk_counter_bytes(int M, int N, int K, int ksplit, int num_cus) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const g16::KSplit ks = g16::ksplit_for(K, ksplit);
-  const g16::Plan p = g16::choose_tile(M, N, K, g16::device_cus());
+  const g16::Plan p = g16::choose_tile(M, N, K, num_cus > 0 ? num_cus : g16::current_cus());
   return g16::splitk_counter_bytes(p, ks.ksplit);
 }
 
 extern "C" int g16_hgemm_f32out(const uint16_t* A, const uint16_t* B, float* C, const float* bias, const float* rscale,
                                 int M, int N, int K, void* stream) {
-  return g16::gemm_launch(A, B, C, false, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream);
+  return g16::gemm_launch(A, B, C, false, bias, rscale, M, N, K, 1, 0, nullptr, 0, nullptr, 0, stream);
 }
 
 extern "C" int g16_hgemm_f16out(const uint16_t* A, const uint16_t* B, uint16_t* C, const float* bias,
                                 const float* rscale, int M, int N, int K, void* stream) {
-  return g16::gemm_launch(A, B, C, true, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream);
+  return g16::gemm_launch(A, B, C, true, bias, rscale, M, N, K, 1, 0, nullptr, 0, nullptr, 0, stream);
 }
 
 extern "C" int g16_hgemm_use_packed(int M, int N, int K, int num_cus) {
@@ -805,29 +832,29 @@ extern "C" int g16_hgemm_use_packed_b(int M, int N, int K, int num_cus) {
 
 extern "C" int g16_hgemm_packed_f32out(const uint16_t* Ap, const uint16_t* B, float* C, const float* bias,
                                       const float* rscale, int M, int N, int K, void* stream) {
-  return g16::gemm_launch(Ap, B, C, false, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true);
+  return g16::gemm_launch(Ap, B, C, false, bias, rscale, M, N, K, 1, 0, nullptr, 0, nullptr, 0, stream, true);
 }
 
 extern "C" int g16_hgemm_packed_f16out(const uint16_t* Ap, const uint16_t* B, uint16_t* C, const float* bias,
                                       const float* rscale, int M, int N, int K, void* stream) {
-  return g16::gemm_launch(Ap, B, C, true, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true);
+  return g16::gemm_launch(Ap, B, C, true, bias, rscale, M, N, K, 1, 0, nullptr, 0, nullptr, 0, stream, true);
 }
 
 extern "C" int g16_hgemm_packed_ab_f32out(const uint16_t* Ap, const uint16_t* Bp, float* C, const float* bias,
                                          const float* rscale, int M, int N, int K, void* stream) {
-  return g16::gemm_launch(Ap, Bp, C, false, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true, true);
+  return g16::gemm_launch(Ap, Bp, C, false, bias, rscale, M, N, K, 1, 0, nullptr, 0, nullptr, 0, stream, true, true);
 }
 
 extern "C" int g16_hgemm_packed_ab_f16out(const uint16_t* Ap, const uint16_t* Bp, uint16_t* C, const float* bias,
                                          const float* rscale, int M, int N, int K, void* stream) {
-  return g16::gemm_launch(Ap, Bp, C, true, bias, rscale, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true, true);
+  return g16::gemm_launch(Ap, Bp, C, true, bias, rscale, M, N, K, 1, 0, nullptr, 0, nullptr, 0, stream, true, true);
 }
 
 extern "C" int g16_hgemm_splitk(const uint16_t* A, const uint16_t* B, void* C, int c_is_f16, const float* bias,
-                                const float* rscale, int M, int N, int K, int ksplit, void* workspace,
+                                const float* rscale, int M, int N, int K, int ksplit, int num_cus, void* workspace,
                                 size_t workspace_bytes, uint32_t* counters, size_t counter_bytes, void* stream) {
-  return g16::gemm_launch(A, B, C, c_is_f16 != 0, bias, rscale, M, N, K, ksplit, workspace, workspace_bytes, counters,
-                          counter_bytes, stream);
+  return g16::gemm_launch(A, B, C, c_is_f16 != 0, bias, rscale, M, N, K, ksplit, num_cus, workspace, workspace_bytes,
+                          counters, counter_bytes, stream);
 }
 
 namespace g16 {
@@ -854,7 +881,8 @@ extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, v
                              size_t counter_bytes, void* stream) {
   // mm_t's GEMM path in one call: the same two launches, and the same result bits, as the
   // separate rowscale and GEMM entry points on the route g16_hgemm_use_packed / g16_hgemm_plan pick
-  if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0 || num_cus <= 0) return G16_E_SHAPE;
+  if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0 || K > g16::kMaxK || N > g16::kMaxN || num_cus <= 0)
+    return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
   if (scratch == nullptr || out == nullptr || (K > 0 && (x == nullptr || w_t == nullptr))) return G16_E_NULL;
   if (!g16::aligned16(scratch)) return G16_E_ALIGN;
@@ -871,8 +899,9 @@ extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, v
                 : g16_rowscale_f16(static_cast<const uint16_t*>(x), y, s, M, K, thresh, stream);
   if (st != G16_OK) return st;
   if (packed)
-    return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, 1, nullptr, 0, nullptr, 0, stream, true);
+    return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, 1, num_cus, nullptr, 0, nullptr, 0, stream,
+                            true);
   const int ks = g16_hgemm_plan(M, N, K, num_cus);
-  return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, ks, workspace, workspace_bytes, counters,
-                          counter_bytes, stream);
+  return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, ks, num_cus, workspace, workspace_bytes,
+                          counters, counter_bytes, stream);
 }

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before libg16.so)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libg16.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -44,9 +44,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_pack_weight": (_I, [_P, _P, _I, _I, _P]),
     "g16_hgemm_packed_ab_f32out": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "g16_hgemm_packed_ab_f16out": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
-    "g16_hgemm_splitk": (_I, [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _SZ, _P, _SZ, _P]),
-    "g16_hgemm_splitk_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
-    "g16_hgemm_splitk_counter_bytes": (_SZ, [_I, _I, _I, _I]),
+    "g16_hgemm_splitk": (_I, [_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P, _SZ, _P]),
+    "g16_hgemm_splitk_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "g16_hgemm_splitk_counter_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "g16_hgemm_plan": (_I, [_I, _I, _I, _I]),
     "g16_skinny_f32in": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P, _SZ, _P]),
     "g16_skinny_f16in": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P, _SZ, _P]),

@@ -95,8 +95,8 @@ def _gemm_route(lib, M: int, N: int, K: int, dev: torch.device) -> tuple:
         else:
             ksplit = lib.g16_hgemm_plan(M, N, K, cus)
             if ksplit > 1:
-                r = ("splitk", scratch, ksplit, lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit),
-                     lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit))
+                r = ("splitk", scratch, ksplit, lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit, cus),
+                     lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit, cus))
             else:
                 r = ("plain", scratch, 1, 0, 0)
         _remember(key, r)

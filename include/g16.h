@@ -20,7 +20,13 @@
  *   - Row-major, contiguous operands: x/A is [M,K], the weight w_t/B is [K,N] (N contiguous),
  *     outputs are [M,N]. K and N must be multiples of 8 and every pointer 16-byte aligned (the
  *     reference's supported() predicate, src/gtx16_fp16/ops.py:29-35, plus the alignment the
- *     16-byte vector loads need). M == 0 or N == 0 is a no-op.
+ *     16-byte vector loads need). M == 0 or N == 0 is a no-op. The GEMM entry points (hgemm_*,
+ *     mm_t_gemm) also need K <= G16_GEMM_MAX_K and N <= G16_GEMM_MAX_N (their operands are
+ *     addressed through 32-bit buffer offsets) and return G16_E_SHAPE beyond them.
+ *   - num_cus: where an entry point plans its launch for a compute-unit count, the GEMM tile and
+ *     hence the split buffers' sizes follow that count. A caller that plans ksplit and sizes the
+ *     split buffers for one count must launch with the same count; num_cus <= 0 means the device's
+ *     own count (the stream's device for a launch, the current device for a size query).
  *   - Split reductions (split-K and skinny paths) take two caller-owned device buffers:
  *       workspace -- fp32 partial sums, at least *_workspace_bytes(); needs no initialisation;
  *       counters  -- per-tile arrival counters, at least *_counter_bytes(); must be all zero
@@ -41,16 +47,20 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 9
+#define G16_ABI_VERSION 10
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
-#define G16_E_SHAPE (-1)       /* negative size, or K or N not a multiple of 8 */
+#define G16_E_SHAPE (-1)       /* negative size, K or N not a multiple of 8, or a GEMM K or N past its limit */
 #define G16_E_ALIGN (-2)       /* a pointer is not 16-byte aligned */
 #define G16_E_NULL (-3)        /* a required pointer is NULL */
 #define G16_E_WORKSPACE (-4)   /* workspace or counters missing or smaller than required */
 #define G16_E_SPLIT (-5)       /* ksplit out of range */
 #define G16_E_DTYPE (-6)       /* unknown dtype code */
+
+/* Size limits of the GEMM entry points (32-bit DMA offsets; see above). */
+#define G16_GEMM_MAX_K ((1 << 22) - 8)
+#define G16_GEMM_MAX_N ((1 << 24) - 8)
 
 /* Semantic constants of the reference. */
 #define G16_SKINNY_MAX_M 8          /* src/gtx16_fp16/kernels.py:253 */
@@ -151,14 +161,16 @@ int g16_hgemm_use_packed_b(int M, int N, int K, int num_cus);
  * writes an fp32 partial tile to the workspace; the last slice to finish a tile sums the partials
  * in slice order, then applies rscale and bias and writes C (fp32, or fp16 when c_is_f16 != 0,
  * so no separate cast pass). ksplit in [1, 256]; ksplit == 1 needs no workspace.
- * g16_hgemm_plan() returns the ksplit this library would choose (1 = the plain GEMM).
+ * g16_hgemm_plan() returns the ksplit this library would choose (1 = the plain GEMM). The tile the
+ * launch runs on, and so the workspace and counter sizes, depend on num_cus (see above): pass the
+ * same num_cus to the plan, the two size queries and the launch.
  */
 int g16_hgemm_splitk(const uint16_t* A, const uint16_t* B, void* C, int c_is_f16,
                      const float* bias, const float* rscale, int M, int N, int K, int ksplit,
-                     void* workspace, size_t workspace_bytes, uint32_t* counters,
+                     int num_cus, void* workspace, size_t workspace_bytes, uint32_t* counters,
                      size_t counter_bytes, void* stream);
-size_t g16_hgemm_splitk_workspace_bytes(int M, int N, int K, int ksplit);
-size_t g16_hgemm_splitk_counter_bytes(int M, int N, int K, int ksplit);
+size_t g16_hgemm_splitk_workspace_bytes(int M, int N, int K, int ksplit, int num_cus);
+size_t g16_hgemm_splitk_counter_bytes(int M, int N, int K, int ksplit, int num_cus);
 int g16_hgemm_plan(int M, int N, int K, int num_cus);
 
 /* ---------------------------------------------------------------------------------------------

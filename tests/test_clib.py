@@ -45,8 +45,8 @@ def test_argument_errors_need_no_gpu(lib):
     assert lib.g16_hgemm_f32out(A + 2, A, A, None, None, 64, 64, 64, None) == -2  # alignment
     assert lib.g16_hgemm_f32out(None, A, A, None, None, 64, 64, 64, None) == -3   # NULL
     assert lib.g16_hgemm_f32out(A, A, A, None, None, 0, 64, 64, None) == 0        # M == 0: no-op
-    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, 64, 64, 1024, 4, None, 0, None, 0, None) == -4
-    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, 64, 64, 1024, 0, None, 0, None, 0, None) == -5
+    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, 64, 64, 1024, 4, 0, None, 0, None, 0, None) == -4
+    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, 64, 64, 1024, 0, 0, None, 0, None, 0, None) == -5
     assert lib.g16_skinny_f32in(A, A, A, None, 9, 64, 64, 1, None, 0, None, 0, None) == -1   # M > 8
     assert lib.g16_skinny_f32in(A, A, A, None, 4, 4096, 4096, 8, A, 1 << 30, None, 0, None) == -4
     assert lib.g16_skinny_f32in(A, A, A + 4, None, 1, 64, 64, 1, None, 0, None, 0, None) == -2  # C alignment
@@ -60,6 +60,47 @@ def test_argument_errors_need_no_gpu(lib):
     assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 64, 256, A, need, None, 0, None, 0, None) == 0
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, 1000.0, None) == -1               # threshold not 2^k
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, -1024.0, None) == -1
+
+
+def test_gemm_size_limits_refused_before_launch(lib):
+    # Operand offsets are 32-bit inside the GEMM's buffer descriptors: K past 2^22 - 8 or N past
+    # 2^24 - 8 would read zeros silently, so every GEMM entry point refuses them (G16_E_SHAPE).
+    A = 0x1000
+    big_k, big_n = (1 << 22), (1 << 24)
+    for fn in (lib.g16_hgemm_f32out, lib.g16_hgemm_f16out, lib.g16_hgemm_packed_f32out,
+               lib.g16_hgemm_packed_ab_f16out):
+        assert fn(A, A, A, None, None, 64, 64, big_k, None) == -1
+        assert fn(A, A, A, None, None, 64, big_n, 64, None) == -1
+    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, 64, 64, big_k, 2, 0, A, 1 << 40, A, 1 << 20, None) == -1
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, big_k, 256, A, 1 << 40, None, 0, None, 0,
+                             None) == -1
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, big_n, 64, 256, A, 1 << 40, None, 0, None, 0,
+                             None) == -1
+
+
+def test_splitk_launch_checks_buffers_against_the_callers_cu_count(lib):
+    # M=300, N=264: 256 CUs take 30 tiles of 32x128 (padded 320 x 384), 10 CUs take 9 tiles of
+    # 128x128 (384 x 384), so the 10-CU plan needs more workspace. A launch for 10 CUs handed the
+    # 256-CU workspace must be refused (it used to plan with the device's own count instead).
+    A = 0x1000
+    M, N, K = 300, 264, 1024
+    ws256 = lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, 256)
+    ws10 = lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, 10)
+    assert ws256 == 2 * 320 * 384 * 4 and ws10 == 2 * 384 * 384 * 4
+    cnt10 = lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, 10)
+    assert cnt10 == 9 * 256 and lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, 256) == 30 * 256
+    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, M, N, K, 2, 10, A, ws256, A, cnt10, None) == -4
+    # counters sized for 10 CUs are too few for the 256-CU grid
+    assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, M, N, K, 2, 256, A, ws256, A, cnt10, None) == -4
+    # num_cus <= 0 in a size query means the current device's count (256 when there is none)
+    assert lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, 0) in (ws256, lib.g16_hgemm_splitk_workspace_bytes(
+        M, N, K, 2, _device_cus()))
+
+
+def _device_cus() -> int:
+    import torch
+
+    return torch.cuda.get_device_properties(0).multi_processor_count if torch.cuda.is_available() else 256
 
 
 def test_plans_and_buffer_sizes(lib):
@@ -92,8 +133,8 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_skinny_workspace_bytes(4, 4096, 4096, ks) == ks * 4 * 4096 * 4
     assert lib.g16_skinny_counter_bytes(4, 4096, 4096, ks) == (4096 // 512) * 256
     assert lib.g16_skinny_workspace_bytes(4, 4096, 4096, 1) == 0
-    assert lib.g16_hgemm_splitk_workspace_bytes(64, 1024, 1024, 1) == 0
-    assert lib.g16_hgemm_splitk_counter_bytes(64, 1024, 1024, 4) > 0
+    assert lib.g16_hgemm_splitk_workspace_bytes(64, 1024, 1024, 1, 0) == 0
+    assert lib.g16_hgemm_splitk_counter_bytes(64, 1024, 1024, 4, 0) > 0
 
 
 def test_fast_extension_matches_the_c_entry_points(lib):

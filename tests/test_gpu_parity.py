@@ -227,13 +227,13 @@ def test_splitk_deterministic_and_matches_plain(lib, cuda, M, K, N):
                                 M, N, K, st) == 0
     ref = oracle.gemm(_np(a), _np(s), _np(b), _np(bias), "float32")
     for ksplit in (2, 3, 8, 16):
-        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit),
-                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit), cuda)
+        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit, 0),
+                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit, 0), cuda)
         outs = []
         for _ in range(10):
             c = torch.empty(M, N, device=cuda)
             assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c.data_ptr(), 0, bias.data_ptr(), s.data_ptr(),
-                                        M, N, K, ksplit, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(),
+                                        M, N, K, ksplit, 0, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(),
                                         st) == 0
             outs.append(c)
         torch.cuda.synchronize()
@@ -252,11 +252,11 @@ def test_splitk_fp16_output(lib, cuda):
     b = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
     bias = randn((N,), seed=2, scale=0.02).to(cuda)
     s = torch.ones(M, device=cuda)
-    ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 8),
-                          lib.g16_hgemm_splitk_counter_bytes(M, N, K, 8), cuda)
+    ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 8, 0),
+                          lib.g16_hgemm_splitk_counter_bytes(M, N, K, 8, 0), cuda)
     c = torch.empty(M, N, dtype=torch.float16, device=cuda)
     assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c.data_ptr(), 1, bias.data_ptr(), s.data_ptr(),
-                                M, N, K, 8, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(),
+                                M, N, K, 8, 0, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(),
                                 _stream(cuda)) == 0
     torch.cuda.synchronize()
     ref = oracle.gemm(_np(a), _np(s), _np(b), _np(bias), "float32")
@@ -282,11 +282,11 @@ def test_small_tiles_odd_and_even_step_counts(lib, cuda, M, N, bk, steps):
         c = torch.empty(M, N, device=cuda)
         assert lib.g16_hgemm_f32out(a.data_ptr(), b.data_ptr(), c.data_ptr(), bias.data_ptr(), s.data_ptr(),
                                     M, N, K, st) == 0
-        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2),
-                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2), cuda)
+        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, 0),
+                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, 0), cuda)
         c2 = torch.empty(M, N, device=cuda)
         assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c2.data_ptr(), 0, bias.data_ptr(), s.data_ptr(),
-                                    M, N, K, 2, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), st) == 0
+                                    M, N, K, 2, 0, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), st) == 0
         torch.cuda.synchronize()
         assert oracle.rel_err(_np(c), ref) <= GEMM_TOL, K
         assert oracle.rel_err(_np(c2), ref) <= GEMM_TOL, K
@@ -360,11 +360,11 @@ def test_abi_rejects_bad_arguments(lib, cuda):
     assert lib.g16_hgemm_f32out(a.data_ptr(), a.data_ptr(), c.data_ptr(), None, None, 64, 64, 60, st) == -1
     assert lib.g16_hgemm_f32out(a.data_ptr() + 2, a.data_ptr(), c.data_ptr(), None, None, 64, 64, 64, st) == -2
     assert lib.g16_hgemm_f32out(None, a.data_ptr(), c.data_ptr(), None, None, 64, 64, 64, st) == -3
-    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 1024, 4,
+    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 1024, 4, 0,
                                 None, 0, None, 0, st) == -4
-    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 1024, 4,
+    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 1024, 4, 0,
                                 c.data_ptr(), c.numel() * 4, None, 0, st) == -4
-    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 64, 0,
+    assert lib.g16_hgemm_splitk(a.data_ptr(), a.data_ptr(), c.data_ptr(), 0, None, None, 64, 64, 64, 0, 0,
                                 None, 0, None, 0, st) == -5
     assert lib.g16_skinny_f32in(a.data_ptr(), a.data_ptr(), c.data_ptr(), None, 9, 64, 64, 1, None, 0, None, 0,
                                 st) == -1
@@ -541,10 +541,10 @@ def test_mm_t_one_call_equals_separate_launches(lib, g, cuda, M, K, N, in_dtype,
         assert rs(x.data_ptr(), y16.data_ptr(), s.data_ptr(), M, K, 1024.0, st) == 0
         ks = lib.g16_hgemm_plan(M, N, K, cus)
         if ks > 1:
-            ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ks),
-                                  lib.g16_hgemm_splitk_counter_bytes(M, N, K, ks), cuda)
+            ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ks, 0),
+                                  lib.g16_hgemm_splitk_counter_bytes(M, N, K, ks, 0), cuda)
             assert lib.g16_hgemm_splitk(y16.data_ptr(), w.data_ptr(), ref.data_ptr(), 1 if f16out else 0,
-                                        bias.data_ptr(), s.data_ptr(), M, N, K, ks, ws.data_ptr(), ws.numel(),
+                                        bias.data_ptr(), s.data_ptr(), M, N, K, ks, 0, ws.data_ptr(), ws.numel(),
                                         cnt.data_ptr(), cnt.numel(), st) == 0
         else:
             fn = lib.g16_hgemm_f16out if f16out else lib.g16_hgemm_f32out

@@ -1,6 +1,8 @@
 """CPU property tests of the launch plans (g16_hgemm_plan, g16_skinny_plan): for any shape the
-plans stay inside the limits the kernels and their buffers are sized for. No GPU needed: the plans
-are host functions of the library."""
+plans stay inside the limits the kernels and their buffers are sized for, and the plan, the tile
+and the buffer sizes the library reports agree with each other. No GPU needed: the plans are host
+functions of the library. The tile is read from the library (its split-buffer sizes), not
+recomputed here."""
 from __future__ import annotations
 
 import pytest
@@ -20,21 +22,21 @@ def _ceil(a: int, b: int) -> int:
     return -(-a // b)
 
 
-def _tiles(M: int, N: int, K: int, num_cus: int) -> int:
-    # the library's tile choice (choose_tile): 32x128, 64x128, 256x256, 256x128 or 128x128
-    if M <= 32:
-        return _ceil(N, 128)
-    if M <= 64:  # two rows of 32x128 tiles while they fill at most half the CUs, else 64x128
-        return 2 * _ceil(N, 128) if 4 * _ceil(N, 128) <= num_cus else _ceil(N, 128)
-    t256 = _ceil(M, 256) * _ceil(N, 256)
-    if M >= 1024 and N >= 256 and 2 * t256 > num_cus:
-        return t256
-    if M >= 1024 and N >= 256 and 8 * t256 > 3 * num_cus:
-        return _ceil(M, 256) * _ceil(N, 128)
-    for bm in (32, 64):  # short K: the smallest 4-wavefront tile whose grid fits one round
-        if K <= 3072 and _ceil(M, bm) * _ceil(N, 128) <= num_cus:
-            return _ceil(M, bm) * _ceil(N, 128)
-    return _ceil(M, 128) * _ceil(N, 128)
+# The GEMM tiles the library has kernels for, by (rows, columns).
+TILES = {(32, 128), (64, 128), (128, 128), (256, 128), (256, 256)}
+
+
+def _tile(lib, M: int, N: int, K: int, num_cus: int) -> tuple[int, int, int]:
+    """(rows, columns, count) of the tile the library runs this shape on for num_cus CUs, read
+    from the library's own size queries for a 2-way split (the tile does not depend on the split):
+    the counters hold one 256-byte line per tile and the partials 2 slices x tile x 4 bytes. (Split
+    slices start on multiples of 64 K, so K < 128 cannot split; the tile rules treat every K up
+    to 3072 alike, so those shapes are asked about at K = 128.)"""
+    Kq = max(K, 128)
+    ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
+    area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
+    bn = 256 if area == 256 * 256 else 128
+    return area // bn, bn, ntiles
 
 
 dims = st.integers(min_value=1, max_value=1 << 15).map(lambda v: v * 8)
@@ -45,16 +47,28 @@ cus = st.sampled_from([64, 120, 256, 304])
 @given(M=st.integers(min_value=9, max_value=70000), N=dims, K=dims, num_cus=cus)
 def test_gemm_plan_limits(lib, M, N, K, num_cus):
     ks = lib.g16_hgemm_plan(M, N, K, num_cus)
-    tiles = _tiles(M, N, K, num_cus)
+    bm, bn, tiles = _tile(lib, M, N, K, num_cus)
+    # one of the compiled tiles, covering the output exactly once
+    assert (bm, bn) in TILES
+    assert tiles == _ceil(M, bm) * _ceil(N, bn)
+    # a 256-row tile only where the rows fill it at least 4 times over; tiles never taller than
+    # needed below that (32-row tiles serve M <= 32)
+    assert bm < 256 or M >= 1024
+    assert M > 32 or bm == 32
+    # the packed route is exactly the unsplit 256-row tiles (their packed stage images)
+    assert lib.g16_hgemm_use_packed(M, N, K, num_cus) == (1 if (bm == 256 and ks == 1) else 0)
     assert 1 <= ks <= 8
     if ks > 1:
         # split only when tiles leave CUs idle, never past one workgroup per CU, >= 256 K a slice
         assert tiles < num_cus
         assert tiles * ks <= num_cus
         assert _ceil(K, ks) >= 256
-        assert lib.g16_hgemm_use_packed(M, N, K, num_cus) == 0
-        assert lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ks) > 0
-        assert lib.g16_hgemm_splitk_counter_bytes(M, N, K, ks) > 0
+        assert lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ks, num_cus) == tiles * ks * bm * bn * 4
+        assert lib.g16_hgemm_splitk_counter_bytes(M, N, K, ks, num_cus) == tiles * 256
+    # the one-call path's scratch holds the cast (row-major, or packed in 256-row blocks of 32-wide
+    # K steps) plus the row scales
+    cast = (_ceil(M, 256) * 256 * _ceil(K, 32) * 32 * 2 if ks == 1 and bm == 256 else M * K * 2)
+    assert lib.g16_mm_t_scratch_bytes(M, N, K, num_cus) == _ceil(cast, 256) * 256 + 4 * M
 
 
 @settings(max_examples=400, deadline=None)
