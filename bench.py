@@ -8,16 +8,21 @@ for M=1 4096x4096 mm_t":
 * ``value`` -- TFLOPS of ``gtx16_fp16.mm_t`` on the 4096^3 configuration with fp32 activations
   (1% of rows pushed to |max| in [2e3, 2e5], so the power-of-two row rescale is exercised) and
   fp16 weights, fp32 out: one step = one mm_t call (rowscale cast + MFMA GEMM), inputs resident in
-  HBM, ``steps`` calls timed between two ``torch.cuda.synchronize()``.
+  HBM, ``steps`` calls timed between two ``torch.cuda.synchronize()``. Before the ``warmup``
+  steps, untimed mm_t calls run for ``--settle-ms`` (default 200 ms) so the timed steps see the
+  part's working clock; the line reports that phase (``clock_settle``) and the shader clock the
+  last timed step's GEMM held (``clock_mhz_last_timed_gemm``, from the kernel's own clock stamps).
 * ``roofline`` -- the GEMM kernel alone (the dominant kernel): 2*M*N*K flop per launch divided by
-  its average launch duration, from a HIP event pair around each GEMM launch of ``steps``
-  (rowscale, GEMM) sequences on the stream the kernels run on, against the fp16 dense MFMA peak.
+  its average launch duration, from a HIP event pair around the GEMM of each of ``steps`` (rowscale,
+  GEMM) launch sequences on the stream the kernels run on, against the fp16 dense MFMA peak; next
+  to it the same kernel launched back to back (``kernel_ms_back_to_back``), which runs at a lower
+  clock (the part is power-limited), each with the shader clock read right after it.
 * ``skinny_m1`` -- the second half of the metric: GB/s of the M=1 K=N=4096 skinny path, kernel
   time from HIP events around a captured HIP graph of launches that rotate over 16 distinct 32 MiB
   weight copies (512 MiB, twice the 256 MB Infinity Cache, so bytes come from HBM), against the
-  8 TB/s HBM peak; plus the per-call mm_t time.
+  8 TB/s HBM peak; plus the per-call mm_t time and its own ``cpu_baseline``.
 * ``cpu_baseline`` -- the reference's CPU path (torch fp32 matmul, the fallback of ops.py:119)
-  on a 4096^3 sample on the host cores of the same run.
+  on a 4096^3 sample on the host cores of the same run (the skinny half: fp32 addmm at M=1).
 
 Inputs are synthetic and seeded on the CPU (x = seed 0, w = 1, bias = 2, outlier rows = 3).
 """
@@ -51,6 +56,10 @@ def parse(argv=None):
     # steps still run slow (measured 869 vs 1001 TFLOPS for 5 vs 200 warm-up steps with the earlier
     # 32x32x16 GEMM).
     ap.add_argument("--warmup", type=int, default=200)
+    # Independently of --warmup, untimed mm_t calls run for this long before the warm-up steps: the
+    # part needs ~35 ms of load to reach its working clock (measured: the first steps take 139-148 us,
+    # ~126 us after 35 ms, flat for the next 3 s). The line reports the phase as `clock_settle`.
+    ap.add_argument("--settle-ms", type=float, default=200.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--report", type=str, default=None, help="also write per-kernel details to this JSON file")
     ap.add_argument("--all", action="store_true",
@@ -92,7 +101,16 @@ def event_time_ms(fn, reps: int, torch) -> float:
     return start.elapsed_time(end) / reps
 
 
-def bench_c4(torch, g, lib, steps: int, warmup: int, dev) -> dict:
+def gemm_clock_mhz(torch, lib, dev) -> float:
+    """Shader clock the latest GEMM launch on the current stream held: its workgroup 0's main-loop
+    shader cycles over 100 MHz reference ticks (g16_gemm_clock)."""
+    buf = torch.zeros(2, dtype=torch.int64, device=dev)
+    _clib_ok(lib.g16_gemm_clock(buf.data_ptr(), torch.cuda.current_stream(dev).cuda_stream))
+    cyc, ticks = buf.tolist()
+    return 100.0 * cyc / ticks if ticks else 0.0
+
+
+def bench_c4(torch, g, lib, steps: int, warmup: int, dev, settle_ms: float = 0.0) -> dict:
     from _inputs import outlier_rows, randn
 
     M = K = N = 4096
@@ -100,6 +118,15 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev) -> dict:
     w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(dev)
     flop = 2.0 * M * N * K
 
+    # clock settle: untimed mm_t calls for settle_ms of wall time, then the warm-up steps
+    settle_calls = 0
+    t_settle = time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < settle_ms:
+        for _ in range(8):
+            g.mm_t(x, w, None, torch.float32)
+        settle_calls += 8
+        torch.cuda.synchronize()
+    settle_wall_ms = (time.perf_counter() - t_settle) * 1e3
     for _ in range(warmup):
         g.mm_t(x, w, None, torch.float32)
     torch.cuda.synchronize()
@@ -108,6 +135,7 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev) -> dict:
         g.mm_t(x, w, None, torch.float32)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    clock_after = gemm_clock_mhz(torch, lib, dev)  # the last timed step's GEMM
 
     # Kernel-level timing on the stream the kernels are launched on (torch's current stream).
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -124,13 +152,12 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev) -> dict:
     def gemm():
         lib.g16_hgemm_packed_f32out(xp.data_ptr(), w.data_ptr(), out.data_ptr(), None, rs.data_ptr(), M, N, K, stream)
 
-    # The same launch sequence as a timed step (rowscale, then GEMM), with an event pair around
-    # every GEMM launch, so the GEMM's average duration is taken over dispatches in the same state
-    # as those of the timed steps (every GEMM dispatch of this run follows a rowscale pass).
-    for _ in range(warmup):
-        rowscale()
-        gemm()
-    torch.cuda.synchronize()
+    # The GEMM's time in the context of the timed steps: the same (rowscale, GEMM) launch sequence,
+    # with an event pair around each GEMM (the mean over `steps` sequences). The part is
+    # power-limited, and its clock follows the average power of the last milliseconds: the rowscale
+    # pass (HBM-bound, little MFMA power) between GEMMs lets it hold a higher clock for the GEMM than
+    # back-to-back GEMM launches get, so both figures are reported, each with the clock the last
+    # GEMM of its batch held (the kernel's own s_memtime / s_memrealtime stamps).
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
     for b, c in evs:
         rowscale()
@@ -139,9 +166,11 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev) -> dict:
         c.record()
     torch.cuda.synchronize()
     gemm_ms = statistics.fmean(b.elapsed_time(c) for b, c in evs)
-    # rowscale alone is short enough that an event pair around each launch inflates it by a few
-    # microseconds: its figure comes from back-to-back launches instead.
-    rowscale_ms = min(event_time_ms(rowscale, steps, torch) for _ in range(3))
+    clock_in_steps = gemm_clock_mhz(torch, lib, dev)
+    # back to back: `steps` launches between one event pair, the median of 3 such batches
+    gemm_b2b_ms = statistics.median(event_time_ms(gemm, steps, torch) for _ in range(3))
+    clock_b2b = gemm_clock_mhz(torch, lib, dev)
+    rowscale_ms = statistics.median(event_time_ms(rowscale, steps, torch) for _ in range(3))
     tflops = flop / (wall_ms * 1e-3) / 1e12
     gemm_tflops = flop / (gemm_ms * 1e-3) / 1e12
     # rowscale: reads 64 MiB fp32, writes 32 MiB fp16 + 16 KiB of scales
@@ -151,10 +180,16 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev) -> dict:
         "tflops": tflops,
         "gemm_kernel_ms": gemm_ms,
         "gemm_kernel_tflops": gemm_tflops,
+        "gemm_clock_mhz": clock_in_steps,
+        "gemm_b2b_ms": gemm_b2b_ms,
+        "gemm_b2b_clock_mhz": clock_b2b,
         "rowscale_kernel_ms": rowscale_ms,
         "rowscale_kernel_gbs": rs_bytes / (rowscale_ms * 1e-3) / 1e9,
         "flop_per_step": flop,
         "outlier_rows": int(round(0.01 * M)),
+        "settle_ms": settle_wall_ms,
+        "settle_calls": settle_calls,
+        "clock_mhz_after_timed": clock_after,
     }
 
 
@@ -585,6 +620,37 @@ def cpu_baseline(torch) -> dict:
     }
 
 
+def cpu_baseline_skinny(torch) -> dict:
+    """The reference's CPU path for the skinny half: torch fp32 x @ w + b (the ops.py:119 /
+    linear.py:69-70 fallback) at M=1, K=N=4096 on the host, in the metric's unit (algorithmic GB/s:
+    x, w as fp16, bias and out; w is held as fp32 on the host, since that is what the fallback
+    multiplies)."""
+    from _inputs import randn
+
+    M, K, N = 1, 4096, 4096
+    x = randn((M, K), seed=0)
+    w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).float()
+    b = randn((N,), seed=2, scale=0.02)
+    torch.addmm(b, x, w)  # warm-up
+    times = []
+    t_end = time.perf_counter() + 3.0
+    while len(times) < 20 or (time.perf_counter() < t_end and len(times) < 2000):
+        t0 = time.perf_counter()
+        torch.addmm(b, x, w)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    nbytes = M * K * 4 + K * N * 2 + N * 4 + M * N * 4
+    return {
+        "value": nbytes / med / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": (f"torch fp32 addmm(b, x, w) at M=1 K=N=4096 on the host (the reference's CPU path), "
+                   f"{med * 1e6:.1f} us per call, 1 warm-up + median of {len(times)} reps; cpu '{cpu_model()}', "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
 def run_only(torch, lib, what: str, steps: int, dev) -> dict:
     """Back-to-back launches of one kernel, for profiling runs."""
     from _inputs import outlier_rows, randn
@@ -695,9 +761,10 @@ def main(argv=None) -> int:
         bench_peak(torch, lib, dev)
         return 0
     configs = bench_all(torch, g, args.steps, dev) if args.all else None
-    c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev)
+    c4 = bench_c4(torch, g, lib, args.steps, args.warmup, dev, args.settle_ms)
     sk = bench_skinny(torch, lib, g, args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch)
+    cpu_sk = None if args.no_cpu_baseline else cpu_baseline_skinny(torch)
     mp = measured_peaks(torch, lib, dev)
     rot = stream_read_rotated(torch, lib, dev)
 
@@ -718,6 +785,9 @@ def main(argv=None) -> int:
         "config": {"workload": "mm_t C4: M=K=N=4096, fp32 activations + pow2 rowscale, fp16 weights, fp32 out",
                    "M": 4096, "K": 4096, "N": 4096, "outlier_rows": c4["outlier_rows"]},
         "pct_of_peak": round(100.0 * c4["tflops"] / MFMA_F16_PEAK_TFLOPS, 2),
+        "clock_settle": {"ms": round(c4["settle_ms"], 1), "mm_t_calls": c4["settle_calls"],
+                         "what": "untimed mm_t calls before the warm-up steps (working clock after ~35 ms of load)"},
+        "clock_mhz_last_timed_gemm": round(c4["clock_mhz_after_timed"]),
         "roofline": {
             "bound": "mfma",
             "kernel": "hgemm_kernel<256x256, packed A> (g16_hgemm_packed_f32out)",
@@ -727,6 +797,10 @@ def main(argv=None) -> int:
             "frac": round(gemm_tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "traffic": traffic_bytes("gemm"),
             "kernel_ms": round(c4["gemm_kernel_ms"], 5),
+            "timing": "event pair around each GEMM of (rowscale, GEMM) launch sequences, as in the timed steps",
+            "clock_mhz": round(c4["gemm_clock_mhz"]),
+            "kernel_ms_back_to_back": round(c4["gemm_b2b_ms"], 5),
+            "clock_mhz_back_to_back": round(c4["gemm_b2b_clock_mhz"]),
             "measured_peak_random_operands": round(mp["mfma_tflops"], 1),
             "measured_peak_clock_mhz": round(mp["mfma_clock_mhz"]),
             "frac_of_measured_peak": round(gemm_tflops / mp["mfma_tflops"], 4),
@@ -758,6 +832,7 @@ def main(argv=None) -> int:
             "bytes_per_launch": sk["bytes_per_launch"],
             "ksplit": sk["ksplit"],
             "mm_t_call_us": round(sk["call_us"], 2),
+            "cpu_baseline": cpu_sk,
         },
         "cpu_baseline": cpu,
     }

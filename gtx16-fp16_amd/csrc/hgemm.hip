@@ -148,6 +148,12 @@ __device__ inline void wait_dma_le() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Shader-clock stamps of the latest GEMM launch: workgroup 0 of every launch records the shader
+// cycles (s_memtime) and 100 MHz reference ticks (s_memrealtime) its main loop took, so
+// 100 MHz * cycles / ticks is the clock the part held while that launch ran (the part is
+// power-limited and its clock moves with load). g16_gemm_clock copies them out.
+__device__ unsigned long long g_loop_clock[2];
+
 // Workgroup barrier without the counter waits __syncthreads() adds: the caller has already waited
 // for exactly the memory operations the next phase depends on. The memory clobber keeps the
 // compiler from moving LDS accesses across it.
@@ -183,6 +189,12 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool stamps = blockIdx.x == 0 && blockIdx.y == 0;  // workgroup 0 records the loop's clock
+  unsigned long long clk_c0 = 0, clk_r0 = 0;
+  if (stamps) {
+    clk_c0 = __builtin_amdgcn_s_memtime();
+    clk_r0 = __builtin_amdgcn_s_memrealtime();
+  }
   const int wm0 = (wave / Cfg::WGN) * Cfg::WTM;
   const int wn0 = (wave % Cfg::WGN) * Cfg::WTN;
 
@@ -442,6 +454,10 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     if (it < nk) step(std::integral_constant<int, 0>{}, it);
   }
   wait_dma_le<0>();  // no DMA may still be writing LDS past this point
+  if (stamps && tid == 0) {
+    g_loop_clock[0] = __builtin_amdgcn_s_memtime() - clk_c0;
+    g_loop_clock[1] = __builtin_amdgcn_s_memrealtime() - clk_r0;
+  }
 
   // ---- split-K: publish this slice, let the last slice reduce ----
   if constexpr (SPLITK) {
@@ -587,6 +603,11 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       }
     }
   }
+}
+
+__global__ void copy_loop_clock(unsigned long long* dst) {
+  dst[0] = g_loop_clock[0];
+  dst[1] = g_loop_clock[1];
 }
 
 enum class Tile { T256, T256N, T128, T64, T32 };
@@ -904,4 +925,11 @@ extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, v
   const int ks = g16_hgemm_plan(M, N, K, num_cus);
   return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, ks, num_cus, workspace, workspace_bytes,
                           counters, counter_bytes, stream);
+}
+
+extern "C" int g16_gemm_clock(unsigned long long* dst, void* stream) {
+  // ordered after the GEMMs already enqueued on `stream`: their stamps are final when it runs
+  if (dst == nullptr) return G16_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(dst) & 7u) != 0) return G16_E_ALIGN;
+  return g16::launch(g16::copy_loop_clock, dim3(1), dim3(1), static_cast<hipStream_t>(stream), dst);
 }

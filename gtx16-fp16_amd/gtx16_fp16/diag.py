@@ -24,6 +24,7 @@ import math
 import torch
 import torch.nn as nn
 
+from .kernels import SKINNY_MAX_M
 from .linear import FastLinear
 from .ops import ROW_SCALE_THRESHOLD
 
@@ -40,7 +41,11 @@ def range_hooks(model: nn.Module, min_features: int = 256, thresh: float = ROW_S
     Returns (stats, handles); stats[name] is updated on every forward:
 
     K, N, w_amax, x_amax, y_amax, rows (rows seen), rows_rescaled (|max| > thresh), max_exponent
-    (largest ceil(log2(|max| / thresh)) seen), nonfinite_rows (rows containing inf or NaN)."""
+    (largest ceil(log2(|max| / thresh)) seen), nonfinite_rows (rows containing inf or NaN).
+
+    rows_rescaled and max_exponent follow mm_t's dispatch (ops.py:78): a call with at most
+    SKINNY_MAX_M rows takes the skinny path, which multiplies the unquantised activations and never
+    rescales, so its rows are counted in ``rows`` (and x_amax) but not as rescaled."""
     stats: dict[str, dict] = {}
     handles = []
 
@@ -57,11 +62,12 @@ def range_hooks(model: nn.Module, min_features: int = 256, thresh: float = ROW_S
                 amax = torch.nan_to_num(x2.abs(), nan=0.0).max(dim=1).values
                 s["rows"] += x2.shape[0]
                 s["nonfinite_rows"] += int((~finite).sum().item())
-                big = amax > thresh
-                s["rows_rescaled"] += int(big.sum().item())
                 top = float(amax.max().item())
                 s["x_amax"] = max(s["x_amax"], top)
-                if math.isfinite(top) and top > thresh:
+                quantised = x2.shape[0] > SKINNY_MAX_M  # the GEMM path, where the rescale applies
+                if quantised:
+                    s["rows_rescaled"] += int((amax > thresh).sum().item())
+                if quantised and math.isfinite(top) and top > thresh:
                     # smallest e with top / 2^e <= thresh
                     m, e = math.frexp(top / thresh)
                     s["max_exponent"] = max(s["max_exponent"], e - 1 if m == 0.5 else e)

@@ -79,9 +79,14 @@ class PreparedLaunch:
 # which every call leaves zero again. One pair is kept per (device, stream) and grown on demand:
 # calls on one stream are ordered, so they can share it; calls on different streams get
 # different buffers.
+#   A buffer that is replaced by a larger one is kept alive, never freed: a HIP graph captured
+# while it was current still writes to it on every replay, and if its memory went back to the
+# caching allocator, a later tensor could be placed there and overwritten by such a replay.
+# Growth doubles the size, so the retired buffers of a key add up to less than its current one.
 _ws_lock = threading.Lock()
 _partials: dict[tuple[int, int], torch.Tensor] = {}
 _counters: dict[tuple[int, int], torch.Tensor] = {}
+_retired: list[torch.Tensor] = []
 _MIN_PARTIAL_BYTES = 1 << 20
 _MIN_COUNTER_BYTES = 64 << 10
 
@@ -93,6 +98,8 @@ def _grown(table: dict, key, nbytes: int, floor: int, device, zero: bool) -> tor
             buf = table.get(key)
             if buf is None or buf.numel() < nbytes:
                 size = max(nbytes, floor, 0 if buf is None else 2 * buf.numel())
+                if buf is not None:
+                    _retired.append(buf)
                 # Allocated (and zero-filled) on the current stream, so ordered before the kernels.
                 make = torch.zeros if zero else torch.empty
                 buf = make(size, dtype=torch.uint8, device=device)
@@ -112,7 +119,9 @@ def split_buffers(device: torch.device, stream: int, partial_bytes: int, counter
 
 
 def release_workspaces() -> None:
-    """Drop every cached split-reduction buffer (they are re-created on demand)."""
+    """Drop every cached split-reduction buffer, the retired ones included (they are re-created on
+    demand). Only safe when no captured HIP graph that used them will be replayed again."""
     with _ws_lock:
         _partials.clear()
         _counters.clear()
+        _retired.clear()

@@ -14,19 +14,25 @@ from .ops import _is_target, _sm_count, is_affected, mm_t, mm_t_prepacked, pack_
 
 
 class FastLinear(nn.Module):
-    """Inference-only linear layer (linear.py:12-76).
+    """Drop-in for ``nn.Linear`` at inference time, backed by the gfx950 kernels (the reference's
+    class of the same name, linear.py:12-76, keeps the same buffers and rules).
 
-    - Weight stored once as fp16, transposed to [in, out] (half the memory of fp32): buffer
-      ``weight_t``; bias kept in fp32: buffer ``bias``.
-    - Small batches (<= 8 rows, e.g. token-by-token generation) compute in fp32 from fp32 inputs.
-    - Larger batches cast inputs to fp16 (rows with |max| > 1024 are first scaled down by a power
-      of two, then scaled back in fp32), multiply on the matrix cores, accumulate in fp32.
-    - Output dtype follows the input dtype (fp32 in -> fp32 out; other dtypes -> fp32).
-    - When autograd is needed or the shape is unsupported, falls back to F.linear.
-    - For large batches on the 256x256 GEMM route the layer also keeps a prepacked copy of its
-      weight (built on first use, rebuilt when ``weight_t`` changes or moves; not part of the
-      state_dict), which the GEMM reads with plain 16-byte loads. It costs one more copy of the
-      fp16 weight; set ``prepack_weight = False`` (class or instance) to do without it.
+    State: ``weight_t`` is the weight transposed to [in_features, out_features] and rounded once to
+    fp16 (nearest-even); ``bias`` stays fp32. Those two buffers are the whole state_dict.
+
+    Which kernel a call reaches depends on its row count M (all leading dimensions flattened):
+    M <= 8 goes to the skinny GEMV, which multiplies the activations exactly as given (fp32 or fp16)
+    in fp32 arithmetic; M > 8 goes to the MFMA GEMM, which first rounds each activation row to fp16
+    after dividing it by a power of two when its largest magnitude exceeds 1024, accumulates in
+    fp32, and multiplies the power of two back in. fp32 and fp16 inputs give outputs of their own
+    dtype; any other input dtype is computed as fp32 and returns fp32. Inputs that need autograd,
+    and shapes the kernels cannot take, are computed by ``F.linear`` instead.
+
+    On the tile-packed GEMM route (large M) the layer also builds, on first use, a copy of its
+    weight in the GEMM's packed layout and keeps it outside the state_dict; it is rebuilt whenever
+    ``weight_t`` is replaced, moved or modified in place. That spends one more fp16 copy of the
+    weight to save the GEMM's transposing LDS reads; ``prepack_weight = False`` (on the class or an
+    instance) turns it off.
     """
 
     prepack_weight = True
@@ -56,7 +62,9 @@ class FastLinear(nn.Module):
         return m
 
     @property
-    def weight(self) -> torch.Tensor:  # some model code reads .weight (e.g. for dtype/device)
+    def weight(self) -> torch.Tensor:
+        """[out_features, in_features] view of ``weight_t``, for callers that inspect a linear
+        layer's ``.weight`` (its shape, device or dtype) as they would on nn.Linear."""
         return self.weight_t.t()
 
     def _decode_entry(self, M: int, dev: torch.device):
@@ -113,7 +121,8 @@ class FastLinear(nn.Module):
         x2 = x.reshape(-1, self.in_features)
         if x2.dtype not in (torch.float16, torch.float32):
             x2 = x2.float()
-        x2 = x2.contiguous()  # fp32 stays fp32: the kernels cast (and rescale large rows) themselves
+        # no cast to fp16 here: the library's rowscale pass does the cast, with the per-row scaling
+        x2 = x2.contiguous()
         if x2.shape[0] == 0 or not supported(x2, self.weight_t):
             y = F.linear(x2.float(), self.weight_t.t().float(), None if self.bias is None else self.bias.float())
         else:

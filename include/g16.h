@@ -195,6 +195,16 @@ size_t g16_skinny_counter_bytes(int M, int N, int K, int ksplit);
 int g16_skinny_plan(int M, int N, int K, int num_cus);
 
 /* ---------------------------------------------------------------------------------------------
+ * Clock of the latest GEMM launch (no counterpart in the reference; a measurement aid for the
+ * benchmark, whose rooflines depend on the clock a power-limited part holds). Every hgemm launch
+ * (any route) has its workgroup 0 record the shader cycles and the 100 MHz reference ticks its main
+ * loop took; g16_gemm_clock enqueues on `stream` a copy of the latest launch's pair into dst[0]
+ * (cycles) and dst[1] (ticks), device memory, 8-byte aligned. Clock in MHz: 100 * dst[0] / dst[1].
+ * Launches on other streams of the device race for the same record.
+ */
+int g16_gemm_clock(unsigned long long* dst, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Peak microbenchmark: the MI355X counterpart of the reference's bench/peak.py:1-63 (which times
  * FFMA, HFMA2 and mma.sync kernels). No counterpart in the kernel ABI: it measures the instruction
  * and bandwidth peaks the benchmark's rooflines divide by, at the clocks the part holds.

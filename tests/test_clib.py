@@ -58,6 +58,8 @@ def test_argument_errors_need_no_gpu(lib):
     assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A + 8, need, None, 0, None, 0, None) == -2
     assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 64, 256, A, need, None, 0, None, 0, None) == -1
     assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 64, 256, A, need, None, 0, None, 0, None) == 0
+    assert lib.g16_gemm_clock(None, None) == -3
+    assert lib.g16_gemm_clock(A + 4, None) == -2
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, 1000.0, None) == -1               # threshold not 2^k
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, -1024.0, None) == -1
 

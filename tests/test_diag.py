@@ -51,3 +51,24 @@ def test_range_hooks_cover_fast_linear_and_accumulate_calls():
     assert s["rows"] == 10 and s["rows_rescaled"] == 0 and s["max_exponent"] == 0
     assert np.isclose(s["w_amax"], fl.weight_t.float().abs().max().item())
     assert risky(stats) == {}
+
+
+def test_range_hooks_do_not_count_rescales_on_the_skinny_path():
+    # mm_t sends calls with <= 8 rows to the skinny path, which never rescales (ops.py:78): their
+    # rows are seen and their max recorded, but nothing is counted as rescaled
+    lin = nn.Linear(256, 256)
+    stats, handles = range_hooks(nn.Sequential(lin))
+    x = torch.randn(8, 256)
+    x[3, 9] = 5.0e4
+    with torch.no_grad():
+        lin(x)
+    s = stats["0"]
+    assert s["rows"] == 8 and s["rows_rescaled"] == 0 and s["max_exponent"] == 0
+    assert np.isclose(s["x_amax"], 5.0e4)
+    x9 = torch.cat([x, torch.randn(1, 256)])  # 9 rows: the GEMM path
+    with torch.no_grad():
+        lin(x9)
+    for h in handles:
+        h.remove()
+    assert s["rows"] == 17 and s["rows_rescaled"] == 1
+    assert s["max_exponent"] == int(oracle.row_exponent(oracle.row_amax(x9.numpy())).max()) == 6

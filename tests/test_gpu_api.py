@@ -206,3 +206,22 @@ def test_graph_capture_replays_match_eager(g, cuda):
             assert torch.equal(out, eager), i
             with torch.no_grad():
                 assert torch.equal(fl(x), eager)
+
+
+def test_gemm_clock_stamps_give_a_plausible_clock(cuda):
+    # g16_gemm_clock: workgroup 0's main-loop shader cycles and 100 MHz ticks of the latest GEMM
+    from gtx16_fp16 import _clib
+
+    lib = _clib.load()
+    a = torch.randn(1024, 1024, device=cuda).half()
+    st = torch.cuda.current_stream(cuda).cuda_stream
+    c = torch.empty(1024, 1024, device=cuda)
+    dst = torch.zeros(2, dtype=torch.int64, device=cuda)
+    assert lib.g16_gemm_clock(dst.data_ptr() + 4, st) == -2
+    assert lib.g16_gemm_clock(None, st) == -3
+    for _ in range(3):
+        assert lib.g16_hgemm_f32out(a.data_ptr(), a.data_ptr(), c.data_ptr(), None, None, 1024, 1024, 1024, st) == 0
+    assert lib.g16_gemm_clock(dst.data_ptr(), st) == 0
+    cyc, ticks = dst.tolist()
+    assert cyc > 0 and ticks > 0
+    assert 300.0 <= 100.0 * cyc / ticks <= 3000.0

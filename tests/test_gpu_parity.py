@@ -213,28 +213,46 @@ def test_massive_activations(g, cuda, M, in_dtype):
     assert oracle.rel_err(_np(y), ref) <= tol
 
 
-# (1024, 1024, 8192) runs the 256x256 tile: 128 output tiles, split over its ping-pong schedule
-@pytest.mark.parametrize("M,K,N", [(64, 1024, 1024), (64, 4096, 1024), (1024, 1024, 1024), (33, 4096, 768),
-                                   (1024, 1024, 8192)])
-def test_splitk_deterministic_and_matches_plain(lib, cuda, M, K, N):
+def _tile(lib, M: int, N: int, K: int, num_cus: int) -> tuple[int, int]:
+    """(rows, columns) of the tile the library runs (M, N, K) on for num_cus CUs, from its
+    split-buffer sizes for a 2-way split (one 256-byte counter line per tile, 2 x tile x 4 bytes of
+    partials per tile)."""
+    Kq = max(K, 128)
+    ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
+    area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
+    bn = 256 if area == 256 * 256 else 128
+    return area // bn, bn
+
+
+# (M, K, N, num_cus, tile): the launch plans its tile for the CU count it is given, so a small count
+# forces the larger tiles onto shapes the device's own count would give smaller ones
+SPLIT_CASES = [(64, 1024, 1024, 256, (32, 128)), (64, 4096, 1024, 256, (32, 128)),
+               (1024, 1024, 1024, 256, (32, 128)), (33, 4096, 768, 256, (32, 128)),
+               (64, 1024, 1024, 16, (64, 128)), (300, 1024, 264, 8, (128, 128)),
+               (1024, 1024, 8192, 256, (256, 128)), (1024, 1024, 8192, 128, (256, 256))]
+
+
+@pytest.mark.parametrize("M,K,N,num_cus,tile", SPLIT_CASES)
+def test_splitk_deterministic_and_matches_plain(lib, cuda, M, K, N, num_cus, tile):
+    assert _tile(lib, M, N, K, num_cus) == tile
     a = randn((M, K), seed=0, dtype=torch.float16).to(cuda)
     b = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
     bias = randn((N,), seed=2, scale=0.02).to(cuda)
     s = torch.ones(M, device=cuda)
     st = _stream(cuda)
     plain = torch.empty(M, N, device=cuda)
-    assert lib.g16_hgemm_f32out(a.data_ptr(), b.data_ptr(), plain.data_ptr(), bias.data_ptr(), s.data_ptr(),
-                                M, N, K, st) == 0
+    assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), plain.data_ptr(), 0, bias.data_ptr(), s.data_ptr(),
+                                M, N, K, 1, num_cus, None, 0, None, 0, st) == 0
     ref = oracle.gemm(_np(a), _np(s), _np(b), _np(bias), "float32")
     for ksplit in (2, 3, 8, 16):
-        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit, 0),
-                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit, 0), cuda)
+        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ksplit, num_cus),
+                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, ksplit, num_cus), cuda)
         outs = []
         for _ in range(10):
             c = torch.empty(M, N, device=cuda)
             assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c.data_ptr(), 0, bias.data_ptr(), s.data_ptr(),
-                                        M, N, K, ksplit, 0, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(),
-                                        st) == 0
+                                        M, N, K, ksplit, num_cus, ws.data_ptr(), ws.numel(), cnt.data_ptr(),
+                                        cnt.numel(), st) == 0
             outs.append(c)
         torch.cuda.synchronize()
         for o in outs[1:]:
@@ -263,30 +281,33 @@ def test_splitk_fp16_output(lib, cuda):
     assert oracle.rel_err(_np(c.float()), ref) <= GEMM_TOL
 
 
-# (M, N, K step) picking the 128x128 (BK 32), 64x128 and 32x128 (BK 64) tiles
-SMALL_TILES = [(300, 264, 32), (64, 1024, 64), (20, 200, 64)]
+# (M, N, K step, num_cus, tile): the 128x128 (BK 32), 64x128 and 32x128 (BK 64) tiles, each forced by
+# the CU count the launch is planned for
+SMALL_TILES = [(300, 264, 32, 8, (128, 128)), (64, 1024, 64, 16, (64, 128)), (20, 200, 64, 256, (32, 128))]
 
 
-@pytest.mark.parametrize("M,N,bk", SMALL_TILES)
+@pytest.mark.parametrize("M,N,bk,num_cus,tile", SMALL_TILES)
 @pytest.mark.parametrize("steps", [1, 2, 3, 5])
-def test_small_tiles_odd_and_even_step_counts(lib, cuda, M, N, bk, steps):
+def test_small_tiles_odd_and_even_step_counts(lib, cuda, M, N, bk, num_cus, tile, steps):
     # The 4-wavefront tiles run their K loop in step pairs plus a tail step for an odd count: whole
     # and ragged last steps, unsplit and in two slices (each slice has its own step count).
     st = _stream(cuda)
     for K in (bk * steps, bk * steps - 8):
+        assert _tile(lib, M, N, K, num_cus) == tile
         a = randn((M, K), seed=steps, dtype=torch.float16).to(cuda)
         b = randn((K, N), seed=steps + 1, scale=0.05, dtype=torch.float16).to(cuda)
         bias = randn((N,), seed=2, scale=0.02).to(cuda)
         s = torch.ones(M, device=cuda)
         ref = oracle.gemm(_np(a), _np(s), _np(b), _np(bias), "float32")
         c = torch.empty(M, N, device=cuda)
-        assert lib.g16_hgemm_f32out(a.data_ptr(), b.data_ptr(), c.data_ptr(), bias.data_ptr(), s.data_ptr(),
-                                    M, N, K, st) == 0
-        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, 0),
-                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, 0), cuda)
+        assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c.data_ptr(), 0, bias.data_ptr(), s.data_ptr(),
+                                    M, N, K, 1, num_cus, None, 0, None, 0, st) == 0
+        ws, cnt = _split_bufs(lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, num_cus),
+                              lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, num_cus), cuda)
         c2 = torch.empty(M, N, device=cuda)
         assert lib.g16_hgemm_splitk(a.data_ptr(), b.data_ptr(), c2.data_ptr(), 0, bias.data_ptr(), s.data_ptr(),
-                                    M, N, K, 2, 0, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), st) == 0
+                                    M, N, K, 2, num_cus, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(),
+                                    st) == 0
         torch.cuda.synchronize()
         assert oracle.rel_err(_np(c), ref) <= GEMM_TOL, K
         assert oracle.rel_err(_np(c2), ref) <= GEMM_TOL, K

@@ -22,12 +22,15 @@ def _cases(n: int = 40):
         K = int(rng.integers(1, 160)) * 8
         N = int(rng.integers(1, 130)) * 8
         out.append((i, M, K, N, bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), bool(rng.integers(0, 2))))
-    # shapes that reach the split-K and tile-packed routes (104 and 106: 256x128 tiles, as 128 tiles
-    # of 256x256 would leave half the CUs idle; 105: a 2-way split of 128x128 tiles)
+    # shapes that reach each route on 256 CUs (test_gpu_routes.py pins the tile of its own cases):
+    # 100, 103: 32x128 tiles split 8 ways; 101, 102: 128x128 unsplit; 104, 106: tile-packed 256x128
+    # (128 tiles of 256x256 would leave half the CUs idle); 105: 256 unsplit 32x128 tiles;
+    # 107: tile-packed 256x256 (144 tiles); 108: 64x128 unsplit (32x128 would need 272 tiles)
     out += [(100, 64, 2048, 512, True, True, False), (101, 1100, 264, 4096, False, True, True),
             (102, 2300, 136, 2048, True, False, True), (103, 33, 4096, 256, False, False, False),
             (104, 2048, 136, 4096, False, False, True), (105, 512, 2048, 2048, True, True, True),
-            (106, 1900, 264, 3896, True, False, False)]
+            (106, 1900, 264, 3896, True, False, False), (107, 2304, 264, 4096, False, True, True),
+            (108, 520, 1024, 2048, True, False, True)]
     return out
 
 

@@ -1,0 +1,137 @@
+"""GPU parity of the public API on the routes the planner picks, and on the BASELINE configurations
+exactly as configured.
+
+* C1: ``matmul(a16, b16)`` at 1024^3 on N(0,1) fp16 from seeds 0 and 1, fp16 out (ops.py:111-119).
+* C3: ``mm_t`` at 64x1024x1024 and 64x4096x1024 (fp16 A, fp32 bias and out) at the split the
+  library plans for this GPU, ten calls bitwise equal (the reference's split-K is not
+  deterministic, README.md:79; tests/test_correctness.py:52-59 checks repeatability).
+* Each split-K tile through ``mm_t``: the 128x128 tile split twice (512x4096x4096), the 64x128
+  tile split twice (64x4096x11008), the 128x128 tile unsplit and split with an odd number of K
+  steps and a ragged last step, and the 32x128 tile of C3. The tile each case runs on is read from
+  the library's split-buffer sizes, so a plan change that moves a case to another tile fails here
+  instead of silently dropping that tile from the tests.
+* The fp16-output golden fixtures (exact rational results, tests/golden/make_golden.py).
+
+Every result is checked against the fp64 oracle: relative Frobenius error <= 1e-3 on the GEMM
+paths, <= 1e-5 on the skinny path, fp16 outputs within one fp16 ulp of the exact fixture.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _inputs import randn
+
+pytestmark = pytest.mark.gpu
+
+GEMM_TOL = 1e-3
+SKINNY_TOL = 1e-5
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(scope="module")
+def g(cuda):
+    import gtx16_fp16
+
+    return gtx16_fp16
+
+
+@pytest.fixture(scope="module")
+def lib(cuda):
+    from gtx16_fp16 import _clib
+
+    return _clib.load()
+
+
+@pytest.fixture(scope="module")
+def cus(cuda):
+    return torch.cuda.get_device_properties(cuda).multi_processor_count
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def _tile(lib, M: int, N: int, K: int, num_cus: int) -> tuple[int, int]:
+    """(rows, columns) of the tile the library runs (M, N, K) on, from its split-buffer sizes for
+    a 2-way split: one 256-byte counter line per tile, 2 x tile x 4 bytes of partials per tile."""
+    Kq = max(K, 128)
+    ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
+    area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
+    bn = 256 if area == 256 * 256 else 128
+    return area // bn, bn
+
+
+def test_c1_matmul_exactly_as_configured(g, cuda):
+    a = randn((1024, 1024), seed=0, dtype=torch.float16)
+    b = randn((1024, 1024), seed=1, dtype=torch.float16)
+    y = g.matmul(a.to(cuda), b.to(cuda))
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float16 and y.shape == (1024, 1024)
+    ref = oracle.mm_t(_np(a), _np(b), None, "float16")
+    assert np.isfinite(_np(y).astype(np.float64)).all()
+    assert oracle.rel_err(_np(y), ref) <= GEMM_TOL
+    # the C1 ids are fp16 and at most ~5 in magnitude: no row is rescaled
+    assert (oracle.row_exponent(oracle.row_amax(_np(a))) == 0).all()
+
+
+# (M, K, N, tile the planner picks on 256 CUs, ksplit it plans)
+ROUTES = [
+    (64, 1024, 1024, (32, 128), 4),      # C3
+    (64, 4096, 1024, (32, 128), 8),      # C3
+    (512, 4096, 4096, (128, 128), 2),    # 128x128 split twice
+    (64, 4096, 11008, (64, 128), 2),     # 64x128 split twice
+    (768, 4056, 4096, (128, 128), 1),    # 128x128 unsplit: 127 K steps, the last one ragged
+    (512, 4056, 4096, (128, 128), 2),    # split: slices of 64 and 63 K steps, the last one ragged
+]
+
+
+@pytest.mark.parametrize("M,K,N,tile,ks", ROUTES)
+def test_planned_route_matches_oracle_and_repeats_bitwise(g, lib, cus, cuda, M, K, N, tile, ks):
+    if cus != 256:
+        pytest.skip(f"the route table is for 256 CUs (this device has {cus})")
+    assert _tile(lib, M, N, K, cus) == tile
+    assert lib.g16_hgemm_plan(M, N, K, cus) == ks
+    x = randn((M, K), seed=0, dtype=torch.float16).to(cuda)
+    w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
+    bias = randn((N,), seed=2, scale=0.02).to(cuda)
+    outs = [g.mm_t(x, w, bias, torch.float32) for _ in range(10)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ref = oracle.mm_t(_np(x), _np(w), _np(bias), "float32")
+    assert oracle.rel_err(_np(outs[0]), ref) <= GEMM_TOL
+    # fp16 output on the same route: the split reduction casts in its epilogue
+    y16 = g.mm_t(x, w, bias, torch.float16)
+    torch.cuda.synchronize()
+    assert oracle.rel_err(_np(y16), oracle.mm_t(_np(x), _np(w), _np(bias), "float16")) <= GEMM_TOL
+
+
+CASES16 = ("skinny_m3", "skinny_m8", "gemm_m12", "gemm_m9", "skinny_tie16", "gemm_tie16")
+
+
+@pytest.mark.parametrize("name", CASES16)
+def test_golden_fp16_output(g, cuda, name):
+    d = np.load(GOLDEN / "mm_t_exact.npz")
+    x, w = d[f"{name}_x"], d[f"{name}_w"]
+    b = d[f"{name}_b"] if f"{name}_b" in d.files else None
+    y = g.mm_t(torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda),
+               None if b is None else torch.from_numpy(b).to(cuda), torch.float16)
+    torch.cuda.synchronize()
+    got = _np(y).view(np.uint16).astype(np.int32)
+    want = d[f"{name}_out16"].astype(np.int32)
+    # same sign, at most one fp16 ulp apart (the kernels accumulate in fp32 in their own order)
+    assert ((got & 0x8000) == (want & 0x8000)).all() or np.all(np.abs(_np(y)) < 2.0 ** -14)
+    assert np.abs(got - want).max() <= 1, name
+    if name == "skinny_tie16":
+        # fp32 result 1 + 2^-11 exactly (the fixture's tie), cast like out.to(fp16): even, 1.0
+        assert int(got[0, 0]) == 0x3C00
+    tol = SKINNY_TOL if x.shape[0] <= 8 else GEMM_TOL
+    y32 = g.mm_t(torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda),
+                 None if b is None else torch.from_numpy(b).to(cuda), torch.float32)
+    torch.cuda.synchronize()
+    assert oracle.rel_err(_np(y32), d[f"{name}_out"]) <= tol

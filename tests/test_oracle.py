@@ -64,6 +64,20 @@ def check_mm_t_exact(mm_t) -> None:
         np.testing.assert_allclose(got, want, rtol=2 ** -22, atol=1e-30, err_msg=name)
 
 
+CASES16 = ("skinny_m3", "skinny_m8", "gemm_m12", "gemm_m9", "skinny_tie16", "gemm_tie16")
+
+
+def check_mm_t_exact16(mm_t) -> None:
+    # fp16 output, bit for bit: the GEMM path's single rounding of the exact result, the skinny
+    # path's fp32-then-fp16 rounding (the *_tie16 cases tell the two apart)
+    d = np.load(GOLDEN / "mm_t_exact.npz")
+    for name in CASES16:
+        b = d[f"{name}_b"] if f"{name}_b" in d.files else None
+        got = np.asarray(mm_t(d[f"{name}_x"], d[f"{name}_w"], b, "float16")).astype(np.float16).view(np.uint16)
+        want = d[f"{name}_out16"]
+        assert np.array_equal(got, want), (name, np.argwhere(got != want)[:4].tolist())
+
+
 def check_identity_and_permutation(gemm) -> None:
     rng = np.random.default_rng(5)
     w = (rng.standard_normal((16, 8))).astype(np.float16)
@@ -116,6 +130,10 @@ def test_rowscale_fixture_and_invariants():
 
 def test_mm_t_matches_exact_rational_results():
     check_mm_t_exact(oracle.mm_t)
+
+
+def test_mm_t_fp16_output_matches_exact_rational_results():
+    check_mm_t_exact16(oracle.mm_t)
 
 
 def test_identity_permutation_and_scale():
@@ -173,6 +191,12 @@ def test_fixture_generator_rounding_agrees_with_known_answers():
         with np.errstate(over="ignore"):
             want = int(np.float64(v).astype(np.float16).view(np.uint16))
         assert mg.fp16_bits_exact(Fraction(float(v))) == want
+    # its fp32 rounding: ties to even at 1 + 2^-24, subnormals, and numpy's fp64 -> fp32 on random values
+    assert mg.fp32_round_exact(1 + Fraction(1, 2 ** 24)) == 1
+    assert mg.fp32_round_exact(1 + Fraction(3, 2 ** 24)) == 1 + Fraction(1, 2 ** 22)
+    assert mg.fp32_round_exact(Fraction(3, 2 ** 151)) == Fraction(1, 2 ** 149)
+    for v in rng.standard_normal(2000) * np.exp(rng.uniform(-100, 80, 2000)):
+        assert float(mg.fp32_round_exact(Fraction(float(v)))) == float(np.float32(v))
 
 
 # ---------------------------------------------------------------------------------------------
@@ -206,7 +230,29 @@ def _mm_t_quantised_skinny(x, w, bias=None, out_dtype="float32"):
     return S.mm_t(x, w, bias, out_dtype)
 
 
+def _gemm_fp16_via_fp32(x, w, bias=None, out_dtype="float32"):
+    # the GEMM path's fp16 output rounded to fp32 first (two roundings instead of one)
+    x = np.asarray(x)
+    if x.shape[0] <= 8 or out_dtype != "float16":
+        return S.mm_t(x, w, bias, out_dtype)
+    return S.fp16_rne(S.mm_t(x, w, bias, "float32"))
+
+
+def _skinny_fp16_single_rounding(x, w, bias=None, out_dtype="float32"):
+    # the skinny path's fp16 output rounded once from the exact sum (no fp32 step)
+    x = np.asarray(x)
+    if x.shape[0] > 8 or out_dtype != "float16":
+        return S.mm_t(x, w, bias, out_dtype)
+    out = np.asarray(x, dtype=np.float64) @ np.asarray(w, dtype=np.float64)
+    if bias is not None:
+        out = out + np.asarray(bias, dtype=np.float64)[None, :]
+    return S.fp16_rne(out)
+
+
 @pytest.mark.parametrize("broken,check", [
+    (_gemm_fp16_via_fp32, check_mm_t_exact16),
+    (_skinny_fp16_single_rounding, check_mm_t_exact16),
+    (_mm_t_without_bias, check_mm_t_exact16),
     (_floor_exponent, check_exponent_kats),
     (_floor_exponent, check_exponent_minimal),
     (_non_strict_exponent, check_exponent_kats),
