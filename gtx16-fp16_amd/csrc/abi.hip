@@ -12,6 +12,7 @@ extern "C" const char* g16_strerror(int status) {
     case G16_E_WORKSPACE: return "workspace missing or too small";
     case G16_E_SPLIT: return "ksplit out of range";
     case G16_E_DTYPE: return "unknown dtype code";
+    case G16_E_TOO_LARGE: return "split does not fit the static scratch of the no-allocation entry point";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

@@ -20,11 +20,19 @@
 //     device-coherent stores and the last slice to arrive (per strip) adds the slices in slice
 //     order. No floating-point atomics: results are bitwise reproducible and C needs no zero-fill
 //     (the reference zero-fills C and accumulates with atomicAdd, kernels.py:205-206).
+#include <mutex>
 #include <type_traits>
 
 #include "g16_common.hpp"
 
 namespace g16 {
+
+// Split buffers of g16_skinny_f32in_noalloc: the arrival counters in the first
+// G16_NOALLOC_COUNTER_BYTES, the fp32 partials in the next G16_NOALLOC_PARTIAL_BYTES. A file-scope
+// device array, so every GPU the library runs on holds its own copy until the process ends; host
+// code reaches it only through the address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[G16_NOALLOC_COUNTER_BYTES + G16_NOALLOC_PARTIAL_BYTES];
+
 namespace {
 
 constexpr int kStripCols = 512;  // 64 lanes x 8 fp16 columns
@@ -284,8 +292,72 @@ int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, i
                 nstrips);
 }
 
+__global__ void clear_words(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Device address of `scratch` on the current device, looked up once per device with that device
+// current. *fresh is set on the call that did the lookup (the counters then need their first
+// clear). Returns nullptr (and the HIP status in *err) when the lookup fails.
+unsigned char* scratch_on_current_device(int* err, bool* fresh) {
+  static std::mutex mu;
+  static void* ptr[64] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *err = static_cast<int>(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= 64) {
+    *err = static_cast<int>(hipErrorInvalidDevice);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  *fresh = false;
+  if (ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      *err = static_cast<int>(e != hipSuccess ? e : hipErrorInvalidSymbol);
+      return nullptr;
+    }
+    ptr[dev] = p;
+    *fresh = true;
+  }
+  return static_cast<unsigned char*>(ptr[dev]);
+}
+
 }  // namespace
 }  // namespace g16
+
+extern "C" int g16_skinny_f32in_noalloc(const float* A, const uint16_t* B, float* C, const float* bias, int M,
+                                        int N, int K, int ksplit, void* stream) {
+  // Sizes are checked before any HIP call: the split must fit the static scratch.
+  if (M < 0 || N < 0 || K < 0 || M > G16_SKINNY_MAX_M || K % 8 != 0 || N % 8 != 0) return G16_E_SHAPE;
+  if (M == 0 || N == 0) return G16_OK;
+  if (ksplit < 1 || ksplit > 4096) return G16_E_SPLIT;
+  const g16::Split sp = g16::split_for(K, ksplit);
+  if (g16::workspace_bytes(M, N, sp.ksplit) > G16_NOALLOC_PARTIAL_BYTES ||
+      g16::counters_needed(M, N, sp.ksplit) > G16_NOALLOC_COUNTER_BYTES)
+    return G16_E_TOO_LARGE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  g16::StreamDeviceScope on_stream_device(st);  // the stream's device is current for the lookup
+  int err = 0;
+  bool fresh = false;
+  unsigned char* base = g16::scratch_on_current_device(&err, &fresh);
+  if (base == nullptr) return err;
+  auto* counters = reinterpret_cast<uint32_t*>(base);
+  if (fresh) {
+    // First use on this device: zero the counters with a kernel (not a memset node, so a caller
+    // capturing this call into a graph replays a plain kernel); every later call leaves them zero.
+    constexpr int kWords = G16_NOALLOC_COUNTER_BYTES / 4;
+    const int rc = g16::launch(g16::clear_words, dim3((kWords + 255) / 256), dim3(256), st, counters, kWords);
+    if (rc != 0) return rc;
+  }
+  return g16::skinny_launch<float>(A, B, C, bias, M, N, K, ksplit, base + G16_NOALLOC_COUNTER_BYTES,
+                                   G16_NOALLOC_PARTIAL_BYTES, counters, G16_NOALLOC_COUNTER_BYTES, stream);
+}
 
 extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
   // Up to one 8-wavefront workgroup per CU, rounded down so that no workgroups are left for a

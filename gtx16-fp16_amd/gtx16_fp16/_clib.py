@@ -53,6 +53,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_skinny_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "g16_skinny_counter_bytes": (_SZ, [_I, _I, _I, _I]),
     "g16_skinny_plan": (_I, [_I, _I, _I, _I]),
+    "g16_skinny_f32in_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "g16_gemm_clock": (_I, [_P, _P]),
     "g16_peak_flops_per_lane_iter": (ctypes.c_double, [_I]),
     "g16_peak_run": (_I, [_I, _I, _I, _P, _P]),

@@ -57,6 +57,7 @@ extern "C" {
 #define G16_E_WORKSPACE (-4)   /* workspace or counters missing or smaller than required */
 #define G16_E_SPLIT (-5)       /* ksplit out of range */
 #define G16_E_DTYPE (-6)       /* unknown dtype code */
+#define G16_E_TOO_LARGE (-7)   /* the split does not fit the static scratch of a _noalloc entry point */
 
 /* Size limits of the GEMM entry points (32-bit DMA offsets; see above). */
 #define G16_GEMM_MAX_K ((1 << 22) - 8)
@@ -193,6 +194,21 @@ int g16_skinny_f16in(const uint16_t* A, const uint16_t* B, float* C, const float
 size_t g16_skinny_workspace_bytes(int M, int N, int K, int ksplit);
 size_t g16_skinny_counter_bytes(int M, int N, int K, int ksplit);
 int g16_skinny_plan(int M, int N, int K, int num_cus);
+
+/* g16_skinny_f32in without caller buffers and without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight decode/serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and result
+ * bits as g16_skinny_f32in minus the four buffer arguments: the split partials and arrival
+ * counters live in a static device array the library holds on every GPU it runs on until the
+ * process ends (G16_NOALLOC_PARTIAL_BYTES of partials, G16_NOALLOC_COUNTER_BYTES of counters:
+ * ksplit * M * N * 4 <= 4 MiB and N <= 131072). A split that does not fit returns
+ * G16_E_TOO_LARGE before any launch; use g16_skinny_f32in with your own buffers then. The first
+ * call on a device also enqueues a small kernel that zeroes the counters. Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other threads) race. */
+#define G16_NOALLOC_PARTIAL_BYTES (4 << 20)
+#define G16_NOALLOC_COUNTER_BYTES (64 << 10)
+int g16_skinny_f32in_noalloc(const float* A, const uint16_t* B, float* C, const float* bias, int M,
+                             int N, int K, int ksplit, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Clock of the latest GEMM launch (no counterpart in the reference; a measurement aid for the

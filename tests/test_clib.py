@@ -58,6 +58,13 @@ def test_argument_errors_need_no_gpu(lib):
     assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A + 8, need, None, 0, None, 0, None) == -2
     assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 64, 256, A, need, None, 0, None, 0, None) == -1
     assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 64, 256, A, need, None, 0, None, 0, None) == 0
+    # the no-allocation skinny variant refuses splits past its static scratch before any HIP call:
+    # 32 slices x 8 x 16384 x 4 bytes = 16 MiB of partials > 4 MiB; N = 131080 needs 257 counter lines
+    assert lib.g16_skinny_f32in_noalloc(A, A, A, None, 8, 16384, 4096, 32, None) == -7
+    assert lib.g16_skinny_f32in_noalloc(A, A, A, None, 1, 131080, 4096, 2, None) == -7
+    assert lib.g16_skinny_f32in_noalloc(A, A, A, None, 9, 64, 64, 1, None) == -1
+    assert lib.g16_skinny_f32in_noalloc(A, A, A, None, 0, 64, 64, 1, None) == 0
+    assert b"static scratch" in lib.g16_strerror(-7)
     assert lib.g16_gemm_clock(None, None) == -3
     assert lib.g16_gemm_clock(A + 4, None) == -2
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, 1000.0, None) == -1               # threshold not 2^k
