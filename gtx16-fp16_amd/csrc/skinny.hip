@@ -40,11 +40,48 @@ constexpr int kWaves = 8;        // wavefronts per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMinRows = 8;      // the plan gives every wavefront at least this many rows
 
-// Rows each lane loads before using any (16 KB of B per wavefront). 16 for every M: with the
-// one-round LDS sum and the plan below, 32 rows at M = 4 lost to 16 (4 x 4096^2: 13.7 vs 12.5 us;
-// 4 x 1024 x 3072: 10.2 vs 7.8 us), M = 3 and 5 were unchanged.
+// Per-M schedule of the kernel, chosen by graph-timed sweeps on MI355X (weights rotated past the
+// Infinity Cache):
+//   rows   -- rows each lane loads per batch (rows x 1 KB per wavefront in flight);
+//   issue  -- a scheduling barrier after the batch's loads, so all of them are issued before the
+//             first multiply (the compiler otherwise starts waiting on the first load part-way
+//             through the batch);
+//   uncond -- the split reduction's partial loads are issued unconditionally (a lane with nothing
+//             to add reads a valid slot and drops it) instead of under a per-lane condition.
+// M = 1 also takes its own LDS sum and reduction (one column per thread, no group bookkeeping,
+// unconditional loads). Per launch, old schedule -> this one, same box: 1 x 4096^2 9.71 -> 9.13 us,
+// 2 x 4096^2 11.24 -> 11.12, 3 x 4096^2 12.71 -> 12.57, 4 x 4096^2 11.82 -> 11.06,
+// 8 x 4096^2 15.90 -> 14.98, 4 x 1024 x 3072 7.82 -> 7.39, 4 x 14336 x 4096 25.25 -> 24.27 (the
+// 4-column groups of M >= 4 gain from unconditional loads; the single columns of M = 2, 3 lost
+// 0.8-1.5 us with them; M = 8 is best with 8 rows and neither change, M = 6 with the old schedule).
 template <int MM>
-constexpr int rows_in_flight() { return 16; }
+struct Sched {
+  static constexpr int rows = 16;
+  static constexpr bool issue = true;
+  static constexpr bool uncond = MM >= 4;
+};
+template <>
+struct Sched<1> {
+  static constexpr int rows = 4;
+  static constexpr bool issue = true;
+  static constexpr bool uncond = true;
+};
+template <>
+struct Sched<6> {  // 6 x 4096^2 14.84 us with the old schedule, 14.92 with the M >= 4 one
+  static constexpr int rows = 16;
+  static constexpr bool issue = false;
+  static constexpr bool uncond = false;
+};
+template <>
+struct Sched<8> {
+  static constexpr int rows = 8;
+  static constexpr bool issue = false;
+  static constexpr bool uncond = false;
+};
+
+// The plan's unit of whole blocks per wavefront: 16 rows (a whole number of batches of every
+// schedule above).
+constexpr int kPlanBlockRows = 16;
 
 __device__ inline float x_at(const float* __restrict__ A, size_t i) { return A[i]; }
 // fp16 activations are read as the aligned dword holding them, so the (wavefront-uniform) load
@@ -92,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     for (int j = 0; j < 8; ++j) acc[m][j] = 0.f;
 
   if (col < N) {
-    constexpr int U = rows_in_flight<MM>();
+    constexpr int U = Sched<MM>::rows;
     const _Float16* bp = B + col;
     int k = k0;
     for (; k + U <= k1; k += U) {
@@ -100,6 +137,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
 #pragma unroll
       for (int u = 0; u < U; ++u)
         w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(k + u) * N));
+      if constexpr (Sched<MM>::issue) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         float a[MM];
@@ -127,6 +165,41 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
         }
       }
     }
+  }
+
+  if constexpr (MM == 1) {
+    // One column per thread: the wavefronts' sums in wavefront order, then (split K) the slices in
+    // slice order, with every partial load issued unconditionally (a thread past N reads column
+    // N - 1 and stores nothing).
+    *reinterpret_cast<float4v*>(&red[wave][0][lane * 8]) = float4v{acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+    *reinterpret_cast<float4v*>(&red[wave][0][lane * 8 + 4]) = float4v{acc[0][4], acc[0][5], acc[0][6], acc[0][7]};
+    __syncthreads();
+    const int t = threadIdx.x;
+    float mine = red[0][0][t];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mine += red[w][0][t];
+    const int c = strip * kStripCols + t;
+    const bool live = c < N;
+    if (ksplit == 1) {
+      if (live) C[c] = mine + (bias != nullptr ? bias[c] : 0.f);
+      return;
+    }
+    if (live) store_coherent(part + static_cast<size_t>(kpart) * N + c, mine);
+    if (!arrive_last_coherent(counters + strip * kCounterStride, static_cast<uint32_t>(ksplit))) return;
+    const float* pc = part + min(c, N - 1);
+    constexpr int kZBatch = 16;
+    float sum = 0.f;
+    for (int z0 = 0; z0 < ksplit; z0 += kZBatch) {
+      float v[kZBatch];
+#pragma unroll
+      for (int b = 0; b < kZBatch; ++b) v[b] = z0 + b < ksplit ? load_coherent(pc + static_cast<size_t>(z0 + b) * N) : 0.f;
+#pragma unroll
+      for (int b = 0; b < kZBatch; ++b)
+        if (z0 + b < ksplit) sum += v[b];
+    }
+    if (live) C[c] = sum + (bias != nullptr ? bias[c] : 0.f);
+    reset_counter(counters + strip * kCounterStride);
+    return;
   }
 
   // Wavefronts -> LDS, then the strip's MM x 512 sums are handed out in groups of kGW consecutive
@@ -193,8 +266,12 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     else store_coherent(part + slot(kpart, i), v);
   };
   auto fetch = [&](int z, int i) -> V {
-    if constexpr (kGW == 4) return load_coherent4(slices, static_cast<uint32_t>(slot(z, i) * 4u));
-    else return load_coherent(part + slot(z, i));
+    // with Sched::uncond, a group that is not live (past N, or past the M rows for M = 5..7) reads
+    // the strip's first slot of slice z instead and its value is dropped
+    const size_t sl = !Sched<MM>::uncond || group_live(i) ? slot(z, i)
+                                                           : static_cast<size_t>(z) * MM * N + strip * kStripCols;
+    if constexpr (kGW == 4) return load_coherent4(slices, static_cast<uint32_t>(sl * 4u));
+    else return load_coherent(part + sl);
   };
 #pragma unroll
   for (int i = 0; i < kGroupsPerThread; ++i)
@@ -213,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     for (int b = 0; b < kZBatch; ++b)
 #pragma unroll
       for (int i = 0; i < kGroupsPerThread; ++i)
-        v[b][i] = (z0 + b < ksplit && group_live(i)) ? fetch(z0 + b, i) : V{};
+        v[b][i] = (z0 + b < ksplit && (Sched<MM>::uncond || group_live(i))) ? fetch(z0 + b, i) : V{};
 #pragma unroll
     for (int b = 0; b < kZBatch; ++b)
 #pragma unroll
@@ -363,7 +440,7 @@ extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
   // Up to one 8-wavefront workgroup per CU, rounded down so that no workgroups are left for a
   // second round (1 x 4096 x 14336: 280 workgroups 28.9 us, 224 workgroups 21.9 us), each
   // wavefront streaming >= min_rows rows; then, within a factor of two below that, a split that
-  // gives every wavefront whole blocks of rows_in_flight() rows (1 x 4096 x 12288: 8 slices
+  // gives every wavefront whole blocks of kPlanBlockRows rows (1 x 4096 x 12288: 8 slices
   // 18.5 us, 10 slices 19.8 us). Chosen from
   // graph-timed sweeps of 4-64 slices over M = 1..8 and K x N in {4096^2, 4096 x 11008,
   // 4096 x 14336, 11008 x 4096}, weights rotated past the Infinity Cache.
@@ -375,7 +452,7 @@ extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
   const int min_rows = M == 1 ? 16 : g16::kMinRows;
   const int cap = K / (g16::kWaves * min_rows) > 1 ? K / (g16::kWaves * min_rows) : 1;
   ks = ks < 1 ? 1 : (ks > cap ? cap : ks);
-  const int block = g16::rows_in_flight<1>();  // the same for every M
+  const int block = g16::kPlanBlockRows;
   for (int d = ks; d >= 1 && 2 * d >= ks; --d) {
     if (K % (g16::kWaves * block * d) == 0) {
       ks = d;
