@@ -386,12 +386,23 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     if (grp == 1) phase_barrier();
     for (int j = 0; j < nk; ++j) {
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(0, j % NSTAGE);
       {
+        // The memory phase interleaves its fragment reads (LDS) and its DMA issue (texture path):
+        // NFRAG / NDMA reads, then one DMA instruction, NDMA times, then any reads left over. On
+        // the 256x256 tile at 4096^3 (12 reads, 4 DMA) this ran 0.4-0.6 % faster than all reads
+        // before all DMA, with the same result bits; every form that issues a DMA before the
+        // first reads ran 1.5-3 % slower.
         const int kd = kbeg + (j + D) * BK;
         const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
+        constexpr int PER = NFRAG / NDMA;
 #pragma unroll
-        for (int d = 0; d < NDMA; ++d) dma_op((j + D) % NSTAGE, kd, ra, rb, d);
+        for (int d = 0; d < NDMA; ++d) {
+#pragma unroll
+          for (int f = d * PER; f < (d + 1) * PER; ++f) frag_op(0, j % NSTAGE, f);
+          dma_op((j + D) % NSTAGE, kd, ra, rb, d);
+        }
+#pragma unroll
+        for (int f = NDMA * PER; f < NFRAG; ++f) frag_op(0, j % NSTAGE, f);
       }
       wait_dma_le<(D - 1) * NDMA>();  // step j+1 has landed (this wavefront's part)
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // step j's fragments are in registers

@@ -32,10 +32,15 @@ class FastLinear(nn.Module):
     weight in the GEMM's packed layout and keeps it outside the state_dict; it is rebuilt whenever
     ``weight_t`` is replaced, moved or modified in place. That spends one more fp16 copy of the
     weight to save the GEMM's transposing LDS reads; ``prepack_weight = False`` (on the class or an
-    instance) turns it off.
+    instance) turns it off. On the same route, layers called one after another with the same input
+    tensor (unmodified, same stream) share its rowscale cast, the last one of which stays cached
+    per stream; ``share_cast = False`` turns that off, and ``ops.release_cast_cache()`` frees it.
     """
 
     prepack_weight = True
+    # Large-batch calls whose input is the same unmodified tensor as the previous such call on the
+    # stream (a transformer's Q, K and V projections) reuse that call's rowscale cast.
+    share_cast = True
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True, device=None):
         super().__init__()
@@ -130,7 +135,8 @@ class FastLinear(nn.Module):
             M = x2.shape[0]
             if self.prepack_weight and M > SKINNY_MAX_M and \
                     prepacked_route(M, self.out_features, self.in_features, x2.device):
-                y = mm_t_prepacked(x2, self.weight_t, self._packed_weight(), self.bias, odt)
+                y = mm_t_prepacked(x2, self.weight_t, self._packed_weight(), self.bias, odt,
+                                   _cast_source=x if self.share_cast else None)
             else:
                 y = mm_t(x2, self.weight_t, self.bias, odt)
         return y.reshape(*shape[:-1], self.out_features).to(out_dtype)

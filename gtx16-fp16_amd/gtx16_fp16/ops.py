@@ -5,6 +5,8 @@ the kernels behind it are the gfx950 ones of libg16.so.
 """
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import _clib
@@ -218,12 +220,51 @@ def pack_weight(w_t: torch.Tensor) -> torch.Tensor:
     return wp
 
 
+# The latest tile-packed rowscale cast per (device index, stream): (weak reference to the tensor the
+# caller named as its source, that tensor's version, (data pointer, M, K, dtype) of the activations
+# cast, owning buffer, packed-cast pointer, row-scales pointer). Consecutive calls that name the same
+# unmodified source (a transformer's Q, K and V projections all read the same hidden states) reuse
+# it instead of casting again. The weak reference makes a freed tensor miss even when a new one
+# gets its address; the version counter makes any in-place write through torch (the tensor or a
+# view of it) miss.
+_cast_cache: dict[tuple[int, int], tuple] = {}
+
+
+def release_cast_cache() -> None:
+    """Drop the cached activation casts (they are rebuilt on demand)."""
+    _cast_cache.clear()
+
+
+def _packed_cast(lib, x2d: torch.Tensor, M: int, K: int, dev: torch.device, stream: int, source=None):
+    """(owner, packed-cast pointer, row-scales pointer) of x2d's tile-packed rowscale cast, enqueued
+    on ``stream``, or the cached one of the previous call on this stream when ``source`` is the same
+    unmodified tensor. Not cached while the stream is being captured into a graph."""
+    key = (dev.index or 0, stream)
+    meta = (x2d.data_ptr(), M, K, x2d.dtype)
+    capturing = torch.cuda.is_current_stream_capturing()
+    if source is not None and not capturing:
+        hit = _cast_cache.get(key)
+        if hit is not None and hit[0]() is source and hit[1] == source._version and hit[2] == meta:
+            return hit[3], hit[4], hit[5]
+    owner, xp, rscale = _cast_scratch(lib.g16_packed_a_bytes(M, K), M, dev)
+    rs_fn = lib.g16_rowscale_pack_f32 if x2d.dtype == torch.float32 else lib.g16_rowscale_pack_f16
+    _clib.check(rs_fn(x2d.data_ptr(), xp, rscale, M, K, ROW_SCALE_THRESHOLD, stream), "rowscale cast")
+    if source is not None and not capturing:
+        _cast_cache[key] = (weakref.ref(source), source._version, meta, owner, xp, rscale)
+    else:
+        _cast_cache.pop(key, None)
+    return owner, xp, rscale
+
+
 def mm_t_prepacked(x2d: torch.Tensor, w_t: torch.Tensor, wp: torch.Tensor, bias: torch.Tensor | None = None,
-                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+                   out_dtype: torch.dtype = torch.float32, _cast_source: torch.Tensor | None = None) -> torch.Tensor:
     """mm_t for a weight that also has its prepacked form ``wp = pack_weight(w_t)``: same contract and
     the same result bits as ``mm_t(x2d, w_t, bias, out_dtype)``. On the large-GEMM route the GEMM
     reads ``wp`` instead of ``w_t`` (plain 16-byte LDS reads for both operands); elsewhere it is
-    exactly mm_t. Check supported(x2d, w_t) first."""
+    exactly mm_t. Check supported(x2d, w_t) first.
+
+    ``_cast_source`` (used by FastLinear) names the tensor x2d was taken from: consecutive calls on
+    one stream with the same unmodified source share one rowscale cast of it."""
     if out_dtype not in (torch.float32, torch.float16):
         raise ValueError(f"out_dtype must be float32 or float16, got {out_dtype}")
     _check_operands(x2d, w_t, bias)
@@ -240,9 +281,7 @@ def mm_t_prepacked(x2d: torch.Tensor, w_t: torch.Tensor, wp: torch.Tensor, bias:
     b = None if bias is None else bias.float().contiguous()
     x2d = _aligned(x2d)
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
-    _scratch, xp, rscale = _cast_scratch(lib.g16_packed_a_bytes(M, K), M, dev)
-    rs_fn = lib.g16_rowscale_pack_f32 if x2d.dtype == torch.float32 else lib.g16_rowscale_pack_f16
-    _clib.check(rs_fn(x2d.data_ptr(), xp, rscale, M, K, ROW_SCALE_THRESHOLD, stream), "rowscale cast")
+    _scratch, xp, rscale = _packed_cast(lib, x2d, M, K, dev, stream, _cast_source)
     fn = lib.g16_hgemm_packed_ab_f32out if out_dtype == torch.float32 else lib.g16_hgemm_packed_ab_f16out
     _clib.check(fn(xp, wp.data_ptr(), out.data_ptr(), None if b is None else b.data_ptr(), rscale, M, N, K, stream),
                 "GEMM")

@@ -112,3 +112,93 @@ def test_fast_linear_large_batch_uses_prepacked_weight_and_tracks_changes(cuda):
         fl.prepack_weight = False
         assert torch.equal(fl(x), y2)
     assert "_wp" not in fl.state_dict() and set(fl.state_dict()) == {"weight_t", "bias"}
+
+
+def _qkv(cuda, K=768, N=768, seed=0):
+    torch.manual_seed(seed)
+    return [FastLinearT.from_linear(nn.Linear(K, N).to(cuda)) for _ in range(3)]
+
+
+FastLinearT = None
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _fast_linear_cls(cuda):
+    global FastLinearT
+    from gtx16_fp16 import FastLinear
+
+    FastLinearT = FastLinear
+
+
+def _unshared(layers, x):
+    for fl in layers:
+        fl.share_cast = False
+    try:
+        with torch.no_grad():
+            return [fl(x) for fl in layers]
+    finally:
+        for fl in layers:
+            fl.share_cast = True
+
+
+def test_shared_cast_across_layers_is_bitwise_the_unshared_result(ops, cuda):
+    # Q, K and V projections of one hidden-states tensor (11264 token rows, on the tile-packed route,
+    # with outlier rows): the second and third layer reuse the first one's rowscale cast
+    layers = _qkv(cuda)
+    x = outlier_rows(randn((11264, 768), seed=3), 0.02, 2e3, 2e5, seed=4).reshape(44, 256, 768).to(cuda)
+    assert ops.prepacked_route(11264, 768, 768, cuda)
+    ops.release_cast_cache()
+    with torch.no_grad():
+        shared = [fl(x) for fl in layers]
+    assert len(ops._cast_cache) == 1
+    want = _unshared(layers, x)
+    torch.cuda.synchronize()
+    for a, b in zip(shared, want):
+        assert torch.equal(a, b)
+    xs = x.reshape(-1, 768)[:1024].cpu().numpy()  # the oracle on the first 1024 rows (outliers among them)
+    ref = oracle.mm_t(xs, layers[1].weight_t.cpu().numpy(), layers[1].bias.cpu().numpy(), "float32")
+    assert oracle.rel_err(shared[1].reshape(-1, 768)[:1024].cpu().numpy(), ref) <= 1e-3
+
+
+def test_shared_cast_misses_after_in_place_write_and_for_a_new_tensor(ops, cuda):
+    layers = _qkv(cuda, seed=1)
+    x = randn((11264, 768), seed=5).to(cuda)
+    assert ops.prepacked_route(11264, 768, 768, cuda)
+    with torch.no_grad():
+        layers[0](x)                      # cached cast of x
+        x.mul_(3000.0)                    # in place: version changes, rows now need the rescale
+        got = layers[1](x)
+    want = _unshared(layers[1:2], x)[0]
+    assert torch.equal(got, want)
+    ptr = x.data_ptr()
+    with torch.no_grad():
+        layers[0](x)
+    del x
+    # a new tensor, often at the same address, with other values: the dead weak reference misses
+    y = randn((11264, 768), seed=6).to(cuda)
+    with torch.no_grad():
+        got = layers[1](y)
+    want = _unshared(layers[1:2], y)[0]
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), f"same address as the cached tensor: {y.data_ptr() == ptr}"
+
+
+def test_no_shared_cast_under_graph_capture(ops, cuda):
+    layers = _qkv(cuda, seed=2)
+    x = randn((11264, 768), seed=7).to(cuda)
+    want = _unshared(layers, x)
+    s = torch.cuda.Stream(cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.stream(s):
+        for fl in layers:
+            fl(x)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            outs = [fl(x) for fl in layers]
+    torch.cuda.current_stream(cuda).wait_stream(s)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs, want):
+            assert torch.equal(a, b)
