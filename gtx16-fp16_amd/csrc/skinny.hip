@@ -6,20 +6,26 @@
 //
 // The path is HBM-bound for small M (arithmetic intensity <= 8 flop/byte): B is streamed exactly
 // once and the design follows from B's layout ([K,N], N contiguous):
-//   * A workgroup (8 wavefronts) owns a 512-column strip of B and a slice of K rows. Each
-//     wavefront takes a contiguous run of rows; one load instruction reads one 1 KB row segment
-//     (64 lanes x 16 bytes = 512 fp16 columns), so every load is fully coalesced and the
-//     activation A[m,k] it multiplies is the same for the whole wavefront: A comes in through
-//     scalar loads, and the vector memory path carries nothing but B.
-//   * Each lane issues 16 row loads before it uses any, so a workgroup has 128 KB of B in flight:
-//     enough to cover HBM latency with up to one workgroup per CU. The
-//     weight is read exactly once, so the loads are non-temporal (measured 7-8 % faster at
-//     4096x4096).
-//   * Reduction is fixed-order: the wavefronts' partial rows are added in wavefront order through
-//     LDS; when K is split over several workgroups, each slice publishes its 512 x M partial with
-//     device-coherent stores and the last slice to arrive (per strip) adds the slices in slice
-//     order. No floating-point atomics: results are bitwise reproducible and C needs no zero-fill
-//     (the reference zero-fills C and accumulates with atomicAdd, kernels.py:205-206).
+//   * A workgroup (8 wavefronts) owns a strip of B's columns and a slice of K rows. Each wavefront
+//     takes a contiguous run of rows, and one load instruction reads 1 KB of them: one 1 KB row
+//     segment with 512-column strips, two 512-byte row segments (lanes 0-31 row k, lanes 32-63
+//     row k+1) with 256-column strips; 16 bytes = 8 fp16 columns a lane. Every load is fully
+//     coalesced and the activations A[m,k] (and A[m,k+1]) it multiplies are the same for the
+//     whole wavefront: A comes in through scalar loads, and the vector memory path carries
+//     nothing but B.
+//   * Each lane issues its batch of row loads before it uses any, so a workgroup has tens of KB
+//     of B in flight: enough to cover HBM latency with up to one workgroup per CU. The weight is
+//     read exactly once, so the loads are non-temporal (measured 7-8 % faster at 4096x4096).
+//   * Reduction is fixed-order: the partial rows are added in order through LDS; when K is split
+//     over several workgroups, each slice publishes its strip x M partial with device-coherent
+//     stores and the last slice to arrive (per strip) adds the slices in slice order. No
+//     floating-point atomics: results are bitwise reproducible and C needs no zero-fill (the
+//     reference zero-fills C and accumulates with atomicAdd, kernels.py:205-206).
+//   * Strip width: for a given grid (about one workgroup per CU) it sets how many slices share a
+//     strip, and the last arriver reads slices x M x width partial sums back through one CU.
+//     Up to N = 8192 the strips are 256 columns (half the slices of 512-column strips and a 4x
+//     smaller read-back; 128-column strips stream worse: 1 x 4096^2 in 8.58-8.62 us, against
+//     9.11-9.16 with 512 columns and 8.91-8.98 with 128), above that 512 (strip_cols).
 #include <mutex>
 #include <type_traits>
 
@@ -35,52 +41,30 @@ static __device__ __align__(256) unsigned char scratch[G16_NOALLOC_COUNTER_BYTES
 
 namespace {
 
-constexpr int kStripCols = 512;  // 64 lanes x 8 fp16 columns
 constexpr int kWaves = 8;        // wavefronts per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMinRows = 8;      // the plan gives every wavefront at least this many rows
 
-// Per-M schedule of the kernel, chosen by graph-timed sweeps on MI355X (weights rotated past the
-// Infinity Cache):
-//   rows   -- rows each lane loads per batch (rows x 1 KB per wavefront in flight);
+// Launch schedule of the kernel:
+//   cols   -- columns of the strip a workgroup owns: 512 (one 1 KB row per load instruction) or
+//             256 (two 512-byte rows per load instruction, lanes 0-31 and 32-63);
+//   loads  -- load instructions each lane issues per batch (loads x 1 KB per wavefront in flight);
 //   issue  -- a scheduling barrier after the batch's loads, so all of them are issued before the
 //             first multiply (the compiler otherwise starts waiting on the first load part-way
 //             through the batch);
 //   uncond -- the split reduction's partial loads are issued unconditionally (a lane with nothing
 //             to add reads a valid slot and drops it) instead of under a per-lane condition.
-// M = 1 also takes its own LDS sum and reduction (one column per thread, no group bookkeeping,
-// unconditional loads). Per launch, old schedule -> this one, same box: 1 x 4096^2 9.71 -> 9.13 us,
-// 2 x 4096^2 11.24 -> 11.12, 3 x 4096^2 12.71 -> 12.57, 4 x 4096^2 11.82 -> 11.06,
-// 8 x 4096^2 15.90 -> 14.98, 4 x 1024 x 3072 7.82 -> 7.39, 4 x 14336 x 4096 25.25 -> 24.27 (the
-// 4-column groups of M >= 4 gain from unconditional loads; the single columns of M = 2, 3 lost
-// 0.8-1.5 us with them; M = 8 is best with 8 rows and neither change, M = 6 with the old schedule).
-template <int MM>
+template <int COLS, int LOADS, bool ISSUE, bool UNCOND>
 struct Sched {
-  static constexpr int rows = 16;
-  static constexpr bool issue = true;
-  static constexpr bool uncond = MM >= 4;
-};
-template <>
-struct Sched<1> {
-  static constexpr int rows = 4;
-  static constexpr bool issue = true;
-  static constexpr bool uncond = true;
-};
-template <>
-struct Sched<6> {  // 6 x 4096^2 14.84 us with the old schedule, 14.92 with the M >= 4 one
-  static constexpr int rows = 16;
-  static constexpr bool issue = false;
-  static constexpr bool uncond = false;
-};
-template <>
-struct Sched<8> {
-  static constexpr int rows = 8;
-  static constexpr bool issue = false;
-  static constexpr bool uncond = false;
+  static constexpr int cols = COLS, loads = LOADS;
+  static constexpr bool issue = ISSUE, uncond = UNCOND;
+  static constexpr int lanes_per_row = COLS / 8;
+  static constexpr int rows_per_load = kWave / lanes_per_row;
+  static constexpr int parts = kWaves * rows_per_load;  // partial rows a workgroup reduces in LDS
+  static_assert(COLS == 256 || COLS == 512, "strip width");
 };
 
-// The plan's unit of whole blocks per wavefront: 16 rows (a whole number of batches of every
-// schedule above).
+// The plan's unit of whole blocks per wavefront: 16 rows.
 constexpr int kPlanBlockRows = 16;
 
 __device__ inline float x_at(const float* __restrict__ A, size_t i) { return A[i]; }
@@ -108,17 +92,22 @@ __device__ inline void fma_row(float (&acc)[MM][8], const float (&a)[MM], u32x4 
     for (int j = 0; j < 8; ++j) acc[m][j] = fmaf(a[m], wf[j], acc[m][j]);
 }
 
-template <typename TX, int MM>
+template <typename TX, int MM, class S>
 __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__ A, const _Float16* __restrict__ B,
                                                           float* __restrict__ C, const float* __restrict__ bias,
                                                           float* __restrict__ part, uint32_t* __restrict__ counters,
                                                           int N, int K, int rows_per_wave, int ksplit, int nstrips) {
-  __shared__ float red[kWaves][MM][kStripCols];  // 16 KB per row of A
+  constexpr int kStripCols = S::cols, kLanesPerRow = S::lanes_per_row, kRowsPerLoad = S::rows_per_load;
+  // Partial sums of every (wavefront, row of its load instructions) pair: 16 KB per row of A.
+  constexpr int kParts = S::parts;
+  __shared__ float red[kParts][MM][kStripCols];
   const int strip = blockIdx.x % nstrips;
   const int kpart = blockIdx.x / nstrips;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = strip * kStripCols + lane * 8;
+  const int sub = lane / kLanesPerRow;  // which row of a load instruction this lane reads
+  const int lcol = (lane % kLanesPerRow) * 8;
+  const int col = strip * kStripCols + lcol;
   const int k0 = (kpart * kWaves + wave) * rows_per_wave;
   const int k1 = min(K, k0 + rows_per_wave);
 
@@ -128,89 +117,112 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[m][j] = 0.f;
 
+  // A[m, r] for row r = k + sub of a load instruction that starts at row k: the instruction's
+  // kRowsPerLoad activations are wavefront-uniform (scalar loads), each lane keeps its own. Rows at
+  // or past k1 are not read (tail of the slice) and give 0.
+  auto act = [&](int k, bool whole, float (&a)[MM]) {
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float v[kRowsPerLoad];
+#pragma unroll
+      for (int r = 0; r < kRowsPerLoad; ++r)
+        v[r] = (whole || k + r < k1) ? x_at(A, static_cast<size_t>(m) * K + k + r) : 0.f;
+      a[m] = v[0];
+#pragma unroll
+      for (int r = 1; r < kRowsPerLoad; ++r) a[m] = sub == r ? v[r] : a[m];
+    }
+  };
+
   if (col < N) {
-    constexpr int U = Sched<MM>::rows;
-    const _Float16* bp = B + col;
+    constexpr int U = S::loads;
+    constexpr int RB = U * kRowsPerLoad;  // rows of a batch
+    const _Float16* bp = B + col + static_cast<size_t>(sub) * N;
     int k = k0;
-    for (; k + U <= k1; k += U) {
+    for (; k + RB <= k1; k += RB) {
       u32x4 w[U];
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(k + u) * N));
-      if constexpr (Sched<MM>::issue) __builtin_amdgcn_sched_barrier(0);
+        w[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(k + u * kRowsPerLoad) * N));
+      if constexpr (S::issue) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         float a[MM];
-#pragma unroll
-        for (int m = 0; m < MM; ++m) a[m] = x_at(A, static_cast<size_t>(m) * K + k + u);
+        act(k + u * kRowsPerLoad, true, a);
         fma_row<MM>(acc, a, w[u]);
       }
     }
     if (k < k1) {
-      // Last, partial block: all U loads still go out together; rows past the slice re-read its last
-      // row and are not used (skipped, not multiplied by zero, so inf/NaN weights cannot leak in).
+      // Last, partial batch: all U loads still go out together; rows past the slice re-read its
+      // last row and are not used (skipped, not multiplied by zero, so inf/NaN weights cannot leak
+      // in).
       u32x4 w[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int r = min(k + u, k1 - 1);
-        w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(r) * N));
+        const int r = min(k + u * kRowsPerLoad + sub, k1 - 1);
+        w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(B + col + static_cast<size_t>(r) * N));
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if (k + u < k1) {
-          float a[MM];
-#pragma unroll
-          for (int m = 0; m < MM; ++m) a[m] = x_at(A, static_cast<size_t>(m) * K + k + u);
-          fma_row<MM>(acc, a, w[u]);
-        }
+        float a[MM];
+        act(k + u * kRowsPerLoad, false, a);
+        if (k + u * kRowsPerLoad + sub < k1) fma_row<MM>(acc, a, w[u]);
       }
     }
   }
 
+  const int part_row = wave * kRowsPerLoad + sub;
   if constexpr (MM == 1) {
-    // One column per thread: the wavefronts' sums in wavefront order, then (split K) the slices in
-    // slice order, with every partial load issued unconditionally (a thread past N reads column
-    // N - 1 and stores nothing).
-    *reinterpret_cast<float4v*>(&red[wave][0][lane * 8]) = float4v{acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
-    *reinterpret_cast<float4v*>(&red[wave][0][lane * 8 + 4]) = float4v{acc[0][4], acc[0][5], acc[0][6], acc[0][7]};
+    // One column per thread (threads 0 .. kStripCols-1, whole wavefronts): the partial rows in
+    // order, then (split K) the slices in slice order, with every partial load issued
+    // unconditionally (a thread past N reads column N - 1 and stores nothing).
+    static_assert(kStripCols % kWave == 0 && kStripCols <= kThreads, "whole wavefronts own the columns");
+    *reinterpret_cast<float4v*>(&red[part_row][0][lcol]) = float4v{acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+    *reinterpret_cast<float4v*>(&red[part_row][0][lcol + 4]) = float4v{acc[0][4], acc[0][5], acc[0][6], acc[0][7]};
     __syncthreads();
     const int t = threadIdx.x;
-    float mine = red[0][0][t];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) mine += red[w][0][t];
+    const bool owner = t < kStripCols;  // uniform per wavefront
     const int c = strip * kStripCols + t;
-    const bool live = c < N;
+    const bool live = owner && c < N;
+    float mine = 0.f;
+    if (owner) {
+      mine = red[0][0][t];
+#pragma unroll
+      for (int w = 1; w < kParts; ++w) mine += red[w][0][t];
+    }
     if (ksplit == 1) {
       if (live) C[c] = mine + (bias != nullptr ? bias[c] : 0.f);
       return;
     }
     if (live) store_coherent(part + static_cast<size_t>(kpart) * N + c, mine);
     if (!arrive_last_coherent(counters + strip * kCounterStride, static_cast<uint32_t>(ksplit))) return;
-    const float* pc = part + min(c, N - 1);
-    constexpr int kZBatch = 16;
-    float sum = 0.f;
-    for (int z0 = 0; z0 < ksplit; z0 += kZBatch) {
-      float v[kZBatch];
+    if (owner) {
+      const float* pc = part + min(c, N - 1);
+      constexpr int kZBatch = 16;
+      float sum = 0.f;
+      for (int z0 = 0; z0 < ksplit; z0 += kZBatch) {
+        float v[kZBatch];
 #pragma unroll
-      for (int b = 0; b < kZBatch; ++b) v[b] = z0 + b < ksplit ? load_coherent(pc + static_cast<size_t>(z0 + b) * N) : 0.f;
+        for (int b = 0; b < kZBatch; ++b) v[b] = z0 + b < ksplit ? load_coherent(pc + static_cast<size_t>(z0 + b) * N) : 0.f;
 #pragma unroll
-      for (int b = 0; b < kZBatch; ++b)
-        if (z0 + b < ksplit) sum += v[b];
+        for (int b = 0; b < kZBatch; ++b)
+          if (z0 + b < ksplit) sum += v[b];
+      }
+      if (live) C[c] = sum + (bias != nullptr ? bias[c] : 0.f);
     }
-    if (live) C[c] = sum + (bias != nullptr ? bias[c] : 0.f);
     reset_counter(counters + strip * kCounterStride);
     return;
   }
 
-  // Wavefronts -> LDS, then the strip's MM x 512 sums are handed out in groups of kGW consecutive
-  // columns of one row (4 for M >= 4, so that the split reduction moves them with 16-byte coherent
-  // accesses; single columns below that, which keeps all 512 threads busy): group g is row
-  // g / (512 / kGW), columns strip*512 + kGW*(g % (512 / kGW)) .., summed over the wavefronts in
+  // Partial rows -> LDS, then the strip's MM x kStripCols sums are handed out in groups of kGW
+  // consecutive columns of one row (4 for M >= 4, so that the split reduction moves them with
+  // 16-byte coherent accesses; single columns below that): group g is row g / (kStripCols / kGW),
+  // columns strip*kStripCols + kGW*(g % (kStripCols / kGW)) .., summed over the partial rows in
   // order. Every row of A goes through LDS in the same round, so one barrier serves all of them.
 #pragma unroll
   for (int m = 0; m < MM; ++m) {
-    *reinterpret_cast<float4v*>(&red[wave][m][lane * 8]) = float4v{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
-    *reinterpret_cast<float4v*>(&red[wave][m][lane * 8 + 4]) = float4v{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
+    *reinterpret_cast<float4v*>(&red[part_row][m][lcol]) = float4v{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+    *reinterpret_cast<float4v*>(&red[part_row][m][lcol + 4]) = float4v{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
   }
   __syncthreads();
   constexpr int kGW = MM >= 4 ? 4 : 1;
@@ -219,7 +231,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
   constexpr int kGroups = MM * kRowGroups;
   constexpr int kGroupsPerThread = (kGroups + kThreads - 1) / kThreads;
   const int t = threadIdx.x;
-  // M = 5..7: the last round of groups covers only part of the threads
+  // groups that do not fill the last round cover only part of the threads
   auto group_in = [&](int i) { return kGroups % kThreads == 0 || t + i * kThreads < kGroups; };
   auto group_row = [&](int i) { return (t + i * kThreads) / kRowGroups; };
   auto group_col = [&](int i) { return strip * kStripCols + ((t + i * kThreads) % kRowGroups) * kGW; };
@@ -236,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     if (group_in(i)) {
       V s = lds_at(0, i);
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) s += lds_at(w, i);
+      for (int w = 1; w < kParts; ++w) s += lds_at(w, i);
       mine[i] = s;
     }
   }
@@ -268,7 +280,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
   auto fetch = [&](int z, int i) -> V {
     // with Sched::uncond, a group that is not live (past N, or past the M rows for M = 5..7) reads
     // the strip's first slot of slice z instead and its value is dropped
-    const size_t sl = !Sched<MM>::uncond || group_live(i) ? slot(z, i)
+    const size_t sl = !S::uncond || group_live(i) ? slot(z, i)
                                                            : static_cast<size_t>(z) * MM * N + strip * kStripCols;
     if constexpr (kGW == 4) return load_coherent4(slices, static_cast<uint32_t>(sl * 4u));
     else return load_coherent(part + sl);
@@ -290,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     for (int b = 0; b < kZBatch; ++b)
 #pragma unroll
       for (int i = 0; i < kGroupsPerThread; ++i)
-        v[b][i] = (z0 + b < ksplit && (Sched<MM>::uncond || group_live(i))) ? fetch(z0 + b, i) : V{};
+        v[b][i] = (z0 + b < ksplit && (S::uncond || group_live(i))) ? fetch(z0 + b, i) : V{};
 #pragma unroll
     for (int b = 0; b < kZBatch; ++b)
 #pragma unroll
@@ -318,18 +330,50 @@ Split split_for(int K, int ksplit) {
 template <typename TX>
 using SkinnyFn = void (*)(const TX*, const _Float16*, float*, const float*, float*, uint32_t*, int, int, int, int, int);
 
-template <typename TX>
-SkinnyFn<TX> skinny_fn(int M) {
+// The schedule of each M and strip width: graph-timed sweeps on MI355X of 2-16 loads per batch,
+// with and without the issue barrier, over M = 1..8 and K x N in {4096^2, 1024 x 3072,
+// 14336 x 4096, 1024^2} (256-column strips) and {4096 x 14336, 4096 x 11008} (512), weights
+// rotated past the Infinity Cache; each entry is the best sum over its shapes (the runner-up is
+// within 1-2 %). The partial-sum loads of M >= 4 are unconditional except for M = 6 and 8.
+template <int MM, int COLS>
+struct SchedFor;
+template <int MM> struct SchedFor<MM, 256> {
+  static constexpr int loads = MM == 1 || MM == 4 || MM == 8 ? 4 : 8;
+  static constexpr bool issue = MM >= 5;
+  using type = Sched<256, loads, issue, MM >= 4 && MM != 6 && MM != 8>;
+};
+template <int MM> struct SchedFor<MM, 512> {
+  static constexpr int loads = MM == 2 || MM == 3 || MM == 7 || MM == 8 ? 16 : 8;
+  static constexpr bool issue = !(MM >= 4 && MM <= 6);
+  using type = Sched<512, loads, issue, MM >= 4 && MM != 6 && MM != 8>;
+};
+
+// Strip width: 256 columns up to N = 8192, 512 above. With few strips the split is deep and the
+// last arriver's read-back (slices x M x strip width) dominates the exchange, which the narrow
+// strips cut 4x (1 x 4096^2: 9.16 -> 8.63 us; 6 x 4096^2: 14.87 -> 10.98); with many strips the
+// split is shallow already and the 1 KB rows stream slightly better (1 x 4096 x 11008: 16.77 us
+// with 512 columns, 16.90 with 256; 8 x 4096 x 14336: 27.3 vs 31.9).
+int strip_cols(int M, int N) {
+  (void)M;
+  return N <= 8192 ? 256 : 512;
+}
+
+template <typename TX, int COLS>
+SkinnyFn<TX> skinny_fn_w(int M) {
   switch (M) {
-    case 1: return skinny_kernel<TX, 1>;
-    case 2: return skinny_kernel<TX, 2>;
-    case 3: return skinny_kernel<TX, 3>;
-    case 4: return skinny_kernel<TX, 4>;
-    case 5: return skinny_kernel<TX, 5>;
-    case 6: return skinny_kernel<TX, 6>;
-    case 7: return skinny_kernel<TX, 7>;
-    default: return skinny_kernel<TX, 8>;
+    case 1: return skinny_kernel<TX, 1, typename SchedFor<1, COLS>::type>;
+    case 2: return skinny_kernel<TX, 2, typename SchedFor<2, COLS>::type>;
+    case 3: return skinny_kernel<TX, 3, typename SchedFor<3, COLS>::type>;
+    case 4: return skinny_kernel<TX, 4, typename SchedFor<4, COLS>::type>;
+    case 5: return skinny_kernel<TX, 5, typename SchedFor<5, COLS>::type>;
+    case 6: return skinny_kernel<TX, 6, typename SchedFor<6, COLS>::type>;
+    case 7: return skinny_kernel<TX, 7, typename SchedFor<7, COLS>::type>;
+    default: return skinny_kernel<TX, 8, typename SchedFor<8, COLS>::type>;
   }
+}
+template <typename TX>
+SkinnyFn<TX> skinny_fn(int M, int cols) {
+  return cols == 256 ? skinny_fn_w<TX, 256>(M) : skinny_fn_w<TX, 512>(M);
 }
 
 size_t workspace_bytes(int M, int N, int ksplit) {
@@ -339,7 +383,31 @@ size_t workspace_bytes(int M, int N, int ksplit) {
 
 size_t counters_needed(int M, int N, int ksplit) {
   if (ksplit <= 1 || M <= 0 || N <= 0) return 0;
-  return counter_bytes(static_cast<size_t>(ceil_div(N, kStripCols)));
+  return counter_bytes(static_cast<size_t>(ceil_div(N, strip_cols(M, N))));
+}
+
+// Up to one 8-wavefront workgroup per CU, rounded down so that no workgroups are left for a second
+// round (1 x 4096 x 14336 on 512-column strips: 280 workgroups 28.9 us, 224 workgroups 21.9 us),
+// each wavefront streaming >= min_rows rows; then, within a factor of two below that, a split that
+// gives every wavefront whole blocks of kPlanBlockRows rows (1 x 4096 x 12288: 8 slices 18.5 us,
+// 10 slices 19.8 us). Chosen from graph-timed sweeps over M = 1..8 and K x N in {4096^2,
+// 4096 x 11008, 4096 x 14336, 11008 x 4096}, weights rotated past the Infinity Cache.
+int plan_with(int M, int N, int K, int num_cus, int cols) {
+  if (N <= 0 || K <= 0 || num_cus <= 0) return 1;
+  const int nstrips = ceil_div(N, cols);
+  int ks = num_cus / nstrips;
+  // M = 1 keeps a full 16-row block per wavefront (6.3 vs 7.2 us at 1x1024x3072); larger M gain
+  // more from the extra slices than they lose to a partial block (10.8 vs 11.3 us at 4x1024x3072).
+  const int min_rows = M == 1 ? 16 : kMinRows;
+  const int cap = K / (kWaves * min_rows) > 1 ? K / (kWaves * min_rows) : 1;
+  ks = ks < 1 ? 1 : (ks > cap ? cap : ks);
+  for (int d = ks; d >= 1 && 2 * d >= ks; --d) {
+    if (K % (kWaves * kPlanBlockRows * d) == 0) {
+      ks = d;
+      break;
+    }
+  }
+  return split_for(K, ks).ksplit;
 }
 
 template <typename TX>
@@ -353,7 +421,8 @@ int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, i
   const Split sp = split_for(K, ksplit);
   // the split partials are addressed through one buffer descriptor: 32-bit byte offsets
   if (workspace_bytes(M, N, sp.ksplit) > 0x7fffffffu) return G16_E_SPLIT;
-  const int nstrips = ceil_div(N, kStripCols);
+  const int cols = strip_cols(M, N);
+  const int nstrips = ceil_div(N, cols);
   float* part = nullptr;
   uint32_t* counters = nullptr;
   if (sp.ksplit > 1) {
@@ -364,7 +433,7 @@ int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, i
     part = static_cast<float*>(ws);
   }
   const dim3 grid(static_cast<unsigned>(nstrips) * static_cast<unsigned>(sp.ksplit)), block(kThreads);
-  return launch(skinny_fn<TX>(M), grid, block, static_cast<hipStream_t>(stream), A,
+  return launch(skinny_fn<TX>(M, cols), grid, block, static_cast<hipStream_t>(stream), A,
                 reinterpret_cast<const _Float16*>(B), C, bias, part, counters, N, K, sp.rows_per_wave, sp.ksplit,
                 nstrips);
 }
@@ -437,30 +506,10 @@ extern "C" int g16_skinny_f32in_noalloc(const float* A, const uint16_t* B, float
 }
 
 extern "C" int g16_skinny_plan(int M, int N, int K, int num_cus) {
-  // Up to one 8-wavefront workgroup per CU, rounded down so that no workgroups are left for a
-  // second round (1 x 4096 x 14336: 280 workgroups 28.9 us, 224 workgroups 21.9 us), each
-  // wavefront streaming >= min_rows rows; then, within a factor of two below that, a split that
-  // gives every wavefront whole blocks of kPlanBlockRows rows (1 x 4096 x 12288: 8 slices
-  // 18.5 us, 10 slices 19.8 us). Chosen from
-  // graph-timed sweeps of 4-64 slices over M = 1..8 and K x N in {4096^2, 4096 x 11008,
-  // 4096 x 14336, 11008 x 4096}, weights rotated past the Infinity Cache.
-  if (N <= 0 || K <= 0 || num_cus <= 0) return 1;
-  const int nstrips = g16::ceil_div(N, g16::kStripCols);
-  int ks = num_cus / nstrips;
-  // M = 1 keeps a full 16-row block per wavefront (6.3 vs 7.2 us at 1x1024x3072); larger M gain
-  // more from the extra slices than they lose to a partial block (10.8 vs 11.3 us at 4x1024x3072).
-  const int min_rows = M == 1 ? 16 : g16::kMinRows;
-  const int cap = K / (g16::kWaves * min_rows) > 1 ? K / (g16::kWaves * min_rows) : 1;
-  ks = ks < 1 ? 1 : (ks > cap ? cap : ks);
-  const int block = g16::kPlanBlockRows;
-  for (int d = ks; d >= 1 && 2 * d >= ks; --d) {
-    if (K % (g16::kWaves * block * d) == 0) {
-      ks = d;
-      break;
-    }
-  }
-  return g16::split_for(K, ks).ksplit;
+  return g16::plan_with(M, N, K, num_cus, g16::strip_cols(M, N));
 }
+
+extern "C" int g16_skinny_strip_cols(int M, int N) { return g16::strip_cols(M, N); }
 
 extern "C" size_t g16_skinny_workspace_bytes(int M, int N, int K, int ksplit) {
   if (K <= 0) return 0;

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before libg16.so)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libg16.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -53,6 +53,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_skinny_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "g16_skinny_counter_bytes": (_SZ, [_I, _I, _I, _I]),
     "g16_skinny_plan": (_I, [_I, _I, _I, _I]),
+    "g16_skinny_strip_cols": (_I, [_I, _I]),
     "g16_skinny_f32in_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "g16_gemm_clock": (_I, [_P, _P]),
     "g16_peak_flops_per_lane_iter": (ctypes.c_double, [_I]),

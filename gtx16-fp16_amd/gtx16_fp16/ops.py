@@ -70,12 +70,14 @@ def _sm_count(device: torch.device) -> int:
 
 def skinny_config(N: int, K: int, sms: int) -> tuple[tuple[int, int, int], int]:
     """Grid and K rows per workgroup of the skinny kernel for ``sms`` compute units
-    (ops.py:45-51): 512-column strips of 8 wavefronts, K split so that about one workgroup lands
-    on every CU."""
-    ksplit = _clib.load().g16_skinny_plan(1, N, K, sms)
+    (ops.py:45-51): column strips of 8 wavefronts (g16_skinny_strip_cols wide), K split so that
+    about one workgroup lands on every CU."""
+    lib = _clib.load()
+    ksplit = lib.g16_skinny_plan(1, N, K, sms)
+    cols = lib.g16_skinny_strip_cols(1, N)
     rows = 0 if K == 0 else -(-(-(-K // ksplit)) // 8) * 8
     ksplit = 1 if K == 0 else -(-K // rows)
-    return ((N + 511) // 512 * ksplit, 1, 1), rows
+    return ((N + cols - 1) // cols * ksplit, 1, 1), rows
 
 
 # (M, N, K, device index) -> the GEMM route mm_t takes for that shape, computed once per shape:

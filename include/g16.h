@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 10
+#define G16_ABI_VERSION 11
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -180,10 +180,12 @@ int g16_hgemm_plan(int M, int N, int K, int num_cus);
  * Replaces skinny_f32in / skinny_f16in (src/gtx16_fp16/kernels.py:212-219) and its launch
  * configuration skinny_config (src/gtx16_fp16/ops.py:45-51,78-84; src/gtx16_fp16/linear.py:49-64).
  * A is read with 16-byte alignment (A must be 16-byte aligned, like B).
- * The kernel streams B once with 16-byte loads; K is split over ksplit workgroups per 512-column
- * strip and reduced deterministically (last arriving workgroup, slice order). C needs no zero-fill.
+ * The kernel streams B once with 16-byte loads; K is split over ksplit workgroups per strip of
+ * g16_skinny_strip_cols(M, N) columns (256 up to N = 8192, 512 above) and reduced
+ * deterministically (last arriving workgroup, slice order). C needs no zero-fill.
  * The split workspace (ksplit * M * N * 4 bytes) must stay below 2 GiB (G16_E_SPLIT otherwise).
- * g16_skinny_plan() returns the ksplit this library would choose for num_cus compute units.
+ * g16_skinny_plan() returns the ksplit this library would choose for num_cus compute units; the
+ * launch grid is ceil(N / strip columns) * ksplit workgroups of 512 threads.
  */
 int g16_skinny_f32in(const float* A, const uint16_t* B, float* C, const float* bias, int M, int N,
                      int K, int ksplit, void* workspace, size_t workspace_bytes, uint32_t* counters,
@@ -194,6 +196,7 @@ int g16_skinny_f16in(const uint16_t* A, const uint16_t* B, float* C, const float
 size_t g16_skinny_workspace_bytes(int M, int N, int K, int ksplit);
 size_t g16_skinny_counter_bytes(int M, int N, int K, int ksplit);
 int g16_skinny_plan(int M, int N, int K, int num_cus);
+int g16_skinny_strip_cols(int M, int N);
 
 /* g16_skinny_f32in without caller buffers and without any allocation. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,

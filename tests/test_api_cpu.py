@@ -10,7 +10,7 @@ import torch
 import torch.nn as nn
 
 import gtx16_fp16 as g
-from gtx16_fp16 import ops
+from gtx16_fp16 import _clib, ops
 
 
 def test_exports_and_version():
@@ -119,8 +119,11 @@ def test_patch_skips_cpu_models_and_respects_filters():
 
 
 def test_skinny_config_covers_k():
-    for N, K in [(4096, 4096), (3072, 1024), (520, 2048), (8, 8)]:
+    lib = _clib.load()
+    for N, K in [(4096, 4096), (3072, 1024), (520, 2048), (8, 8), (14336, 4096)]:
         (gx, gy, gz), rows = ops.skinny_config(N, K, 256)
-        nstrips = (N + 511) // 512
+        cols = lib.g16_skinny_strip_cols(1, N)
+        assert cols == (256 if N <= 8192 else 512)
+        nstrips = (N + cols - 1) // cols
         assert gy == gz == 1 and gx % nstrips == 0
         assert (gx // nstrips) * rows >= K > (gx // nstrips - 1) * rows

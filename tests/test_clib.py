@@ -134,13 +134,17 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_hgemm_use_packed_b(2048, 4096, 4096, 256) == 1
     assert lib.g16_hgemm_use_packed_b(4096, 4096, 4096, 256) == 1
     assert lib.g16_hgemm_use_packed_b(1536, 4096, 4096, 256) == 0    # 128x128 tiles, not packed
-    # skinny: whole 16-row blocks per wavefront, at most one workgroup per CU
-    assert lib.g16_skinny_plan(1, 4096, 4096, 256) == 32
-    assert lib.g16_skinny_plan(4, 4096, 4096, 256) == 32
+    # skinny: 256-column strips up to N = 8192, 512 above; whole 16-row blocks per wavefront, at
+    # most one workgroup per CU
+    assert lib.g16_skinny_strip_cols(1, 4096) == 256 and lib.g16_skinny_strip_cols(8, 8192) == 256
+    assert lib.g16_skinny_strip_cols(1, 8200) == 512 and lib.g16_skinny_strip_cols(4, 14336) == 512
+    assert lib.g16_skinny_plan(1, 4096, 4096, 256) == 16             # 16 strips x 16 slices
+    assert lib.g16_skinny_plan(4, 4096, 4096, 256) == 16
     assert lib.g16_skinny_plan(1, 14336, 4096, 256) == 8             # 28 strips: 8 x 28 <= 256
     ks = lib.g16_skinny_plan(4, 4096, 4096, 256)
     assert lib.g16_skinny_workspace_bytes(4, 4096, 4096, ks) == ks * 4 * 4096 * 4
-    assert lib.g16_skinny_counter_bytes(4, 4096, 4096, ks) == (4096 // 512) * 256
+    assert lib.g16_skinny_counter_bytes(4, 4096, 4096, ks) == (4096 // 256) * 256
+    assert lib.g16_skinny_counter_bytes(4, 14336, 4096, 8) == (14336 // 512) * 256
     assert lib.g16_skinny_workspace_bytes(4, 4096, 4096, 1) == 0
     assert lib.g16_hgemm_splitk_workspace_bytes(64, 1024, 1024, 1, 0) == 0
     assert lib.g16_hgemm_splitk_counter_bytes(64, 1024, 1024, 4, 0) > 0

@@ -75,7 +75,9 @@ def test_gemm_plan_limits(lib, M, N, K, num_cus):
 @given(M=st.integers(min_value=1, max_value=8), N=dims, K=dims, num_cus=cus)
 def test_skinny_plan_limits(lib, M, N, K, num_cus):
     ks = lib.g16_skinny_plan(M, N, K, num_cus)
-    strips = _ceil(N, 512)
+    cols = lib.g16_skinny_strip_cols(M, N)
+    assert cols in (256, 512)
+    strips = _ceil(N, cols)
     assert ks >= 1
     # every wavefront gets rows (8 wavefronts per slice), and the grid stays within one
     # workgroup per CU whenever the strips alone do
@@ -84,3 +86,5 @@ def test_skinny_plan_limits(lib, M, N, K, num_cus):
         assert strips * ks <= num_cus
     ws = lib.g16_skinny_workspace_bytes(M, N, K, ks)
     assert ws == (0 if ks == 1 else ks * M * N * 4)
+    # one 256-byte counter line per strip
+    assert lib.g16_skinny_counter_bytes(M, N, K, ks) == (0 if ks == 1 else strips * 256)
