@@ -35,6 +35,11 @@
 //     workgroup b is mapped to tile (b % 8) * (T / 8) + b / 8, giving each XCD a contiguous run
 //     of tiles, which a grouped (GROUP_M rows at a time) order turns into a compact 2-D block
 //     that shares A rows and B columns in that XCD's L2.
+//   * Resident A (the unsplit 32x128 tile with K <= kResidentSteps * 64, mm_t's GEMM path in one
+//     launch): the workgroup reads its 32 rows of the fp32/fp16 activations itself, computes each
+//     row's scale (rowscale_math.hpp, the rowscale kernel's arithmetic) and writes the scaled fp16
+//     rows into LDS as the stage images of every K step, which then stay resident; only B streams
+//     through the ring. No fp16 copy of A goes to HBM and no separate rowscale launch runs.
 //   * Split-K: slice z of tile t covers K range [z*kchunk, (z+1)*kchunk). Every slice stores its
 //     fp32 accumulators to the workspace in the lanes' own register order (fully coalesced 16-byte
 //     device-coherent stores); the last slice to arrive adds all slices in slice order and runs the
@@ -43,6 +48,7 @@
 #include <type_traits>
 
 #include "g16_common.hpp"
+#include "rowscale_math.hpp"
 
 namespace g16 {
 namespace {
@@ -135,6 +141,9 @@ struct TileCfg {
   }
 };
 
+// K steps the resident-A tile keeps in LDS: 20 x 4 KB of A plus the 64 KB B ring (K <= 1280).
+constexpr int kResidentSteps = 20;
+
 using Cfg256 = TileCfg<256, 256, 32, 2, 4, 4, true>;  // 8 wavefronts (two per SIMD), 4-stage ring, 128 KB
 using Cfg256n = TileCfg<256, 128, 32, 2, 4, 4, true>;  // the same schedule on half the columns, 96 KB
 using Cfg128 = TileCfg<128, 128, 32, 2, 2, 4>;  // 64 KB: two workgroups per CU
@@ -154,21 +163,46 @@ __device__ inline void wait_dma_le() {
 // power-limited and its clock moves with load). g16_gemm_clock copies them out.
 __device__ unsigned long long g_loop_clock[2];
 
+// Largest of v over the 64 lanes, in every lane: DPP within each row of 16 lanes, then the four
+// rows' results through scalar reads. (max is exact, so any order gives the rowscale kernel's
+// value.)
+__device__ inline float wave_max(float v) {
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0xb1>{}));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4e>{}));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x124>{}));  // row_ror:4
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x128>{}));  // row_ror:8
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
 // Workgroup barrier without the counter waits __syncthreads() adds: the caller has already waited
 // for exactly the memory operations the next phase depends on. The memory clobber keeps the
 // compiler from moving LDS accesses across it.
 __device__ inline void phase_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <class Cfg, bool OUT_F16, bool SPLITK, bool PACKED_A = false, bool PACKED_B = false>
+// RESIDENT: A is unused; the kernel casts X (fp32 when x_f32, else fp16; threshold 2^texp) itself
+// into resident LDS stages (the 32x128 tile, unsplit, K <= kResidentSteps * BK).
+template <class Cfg, bool OUT_F16, bool SPLITK, bool PACKED_A = false, bool PACKED_B = false, bool RESIDENT = false>
 __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
                                                          void* __restrict__ Cv, const float* __restrict__ bias,
                                                          const float* __restrict__ rscale, float* __restrict__ part,
                                                          uint32_t* __restrict__ counters, int M, int N, int K,
-                                                         int kchunk, int ksplit, int ntm, int ntn) {
+                                                         int kchunk, int ksplit, int ntm, int ntn,
+                                                         const void* __restrict__ X, int x_f32, int texp) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN, MB = Cfg::MB, MK = Cfg::MK;
   constexpr int BK = Cfg::BK, NSTAGE = Cfg::NSTAGE;
-  __shared__ __attribute__((aligned(1024))) unsigned char sA[NSTAGE][Cfg::A_BYTES];
+  static_assert(!RESIDENT || (Cfg::BM == 32 && Cfg::BK == 64 && Cfg::WAVES == 4 && !SPLITK && !PACKED_A && !PACKED_B),
+                "resident A: the unsplit 32x128 tile");
+  constexpr int A_STAGES = RESIDENT ? kResidentSteps : NSTAGE;
+  __shared__ __attribute__((aligned(1024))) unsigned char sA[A_STAGES][Cfg::A_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char sB[NSTAGE][Cfg::B_BYTES];
+  __shared__ float s_scale[RESIDENT ? BM : 1];
   const uint32_t sA_lds = lds_base(&sA[0][0]), sB_lds = lds_base(&sB[0][0]);
 
   // ---- tile assignment (XCD-aware, grouped) ----
@@ -324,10 +358,12 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   constexpr int KS = BK / MK;
   half8 af[2][KS][TM], bf[2][KS][TN];
   // fragment read f of a step: f = ks * (TM + TN) + (i < TM ? i : TM + j)
-  auto frag_op = [&](int buf, int st, int f) {
+  // st: the ring stage of B (and of A); sta: A's stage where it differs (the resident-A tile keeps
+  // every K step's A image in its own stage)
+  auto frag_op = [&](int buf, int st, int f, int sta = -1) {
     const int ks = f / (TM + TN), w = f % (TM + TN);
     if (w < TM) {
-      af[buf][ks][w] = *reinterpret_cast<const half8*>(&sA[st][a_off(w, ks)]);
+      af[buf][ks][w] = *reinterpret_cast<const half8*>(&sA[sta < 0 ? st : sta][a_off(w, ks)]);
     } else if constexpr (PACKED_B) {
       // B^T stored [n][k] like A: one 16-byte read gives lane l the k-run of column l%32.
       const int j = w - TM;
@@ -343,9 +379,9 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       bf[buf][ks][j] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   };
-  auto read_frags = [&](int buf, int st) {
+  auto read_frags = [&](int buf, int st, int sta = -1) {
 #pragma unroll
-    for (int f = 0; f < KS * (TM + TN); ++f) frag_op(buf, st, f);
+    for (int f = 0; f < KS * (TM + TN); ++f) frag_op(buf, st, f, sta);
   };
   // MFMA m of a step: m = (ks * TM + i) * TN + jj, with j = jj on even i and TN - 1 - jj on odd i
   // (a snake over the blocks), so that consecutive MFMAs always share one operand register: the
@@ -359,6 +395,77 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
     else
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
+  };
+
+  // Resident A: this tile's BM rows of X, scaled and cast to fp16, written as the stage images of
+  // all nk K steps (row r's logical 16-byte chunk c of step j at stage j, byte r * BK * 2 +
+  // ((c ^ swz_a(r)) * 16): where the DMA would put it), zeros past K and past M; s_scale[r] gets
+  // the row's scale. Wavefront w casts rows 8w .. 8w+7, all of their loads in flight at once.
+  auto cast_resident = [&](auto* xp) {
+    if constexpr (RESIDENT) {
+      using TX = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+      constexpr int EPC = 16 / static_cast<int>(sizeof(TX));                  // elements per input chunk
+      constexpr int CM = (kResidentSteps * BK / EPC + kWave - 1) / kWave;      // input chunks per lane and row
+      constexpr int RPW = BM / Cfg::WAVES;                                     // rows per wavefront
+      constexpr int RB = RPW;                                                  // rows in flight
+      const int nch = K / EPC;
+      for (int b = 0; b < RPW; b += RB) {
+        u32x4 v[RB][CM];
+        float am[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          const int grow = m0 + wave * RPW + b + i;
+          const u32x4* xr = reinterpret_cast<const u32x4*>(xp + static_cast<size_t>(min(grow, M - 1)) * K);
+          am[i] = 0.f;
+#pragma unroll
+          for (int c = 0; c < CM; ++c) {
+            const int idx = lane + c * kWave;
+            v[i][c] = (grow < M && idx < nch) ? xr[idx] : u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int c = 0; c < CM; ++c) am[i] = chunk_absmax(am[i], v[i][c], TX{});
+#pragma unroll
+        for (int i = 0; i < RB; ++i) am[i] = wave_max(am[i]);
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          const int r = wave * RPW + b + i;
+          int e;
+          float sc;
+          row_exponent(am[i], texp, e, sc);
+          if (lane == 0) s_scale[r] = sc;
+          unsigned char* row_base = &sA[0][0] + r * (BK * 2);
+          const int sw = Cfg::swz_a(r);
+#pragma unroll
+          for (int c = 0; c < CM; ++c) {
+            const int idx = lane + c * kWave;
+            if (idx < nch) {
+              if constexpr (EPC == 8) {
+                // elements 8 idx .. 8 idx + 7: step idx / 8, logical chunk idx % 8
+                *reinterpret_cast<u32x4*>(row_base + (idx >> 3) * Cfg::A_BYTES + (((idx & 7) ^ sw) << 4)) =
+                    cast_scaled(v[i][c], e, TX{});
+              } else {
+                // elements 4 idx .. 4 idx + 3: half idx % 2 of output chunk idx / 2
+                const int oc = idx >> 1;
+                *reinterpret_cast<u32x2*>(row_base + (oc >> 3) * Cfg::A_BYTES + (((oc & 7) ^ sw) << 4) + ((idx & 1) << 3)) =
+                    cast_scaled(v[i][c], e, TX{});
+              }
+            }
+          }
+        }
+      }
+      // zeros for the columns past K in the last step (K % BK != 0)
+      const int oc0 = K / 8, oc1 = nk * (BK / 8);
+      for (int i = 0; i < RPW; ++i) {
+        const int r = wave * RPW + i;
+        unsigned char* row_base = &sA[0][0] + r * (BK * 2);
+        for (int oc = oc0 + lane; oc < oc1; oc += kWave)
+          *reinterpret_cast<u32x4*>(row_base + (oc >> 3) * Cfg::A_BYTES + (((oc & 7) ^ Cfg::swz_a(r)) << 4)) =
+              u32x4{0u, 0u, 0u, 0u};
+      }
+    }
   };
 
   static_assert(NSTAGE >= 3, "three stages at least");
@@ -423,12 +530,29 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     // The three streams are cut into PARTS slices issued round-robin (DMA, MFMAs, LDS reads), so
     // no wavefront front-loads its DMA and the memory pipes see a steady trickle between barriers.
     constexpr int LAG = NSTAGE - 2;
-    constexpr int PARTS = NDMA;
-    if (nk > 0) {
+    // DMA instructions per step: A and B, or B alone with resident A
+    constexpr int DMA0 = RESIDENT ? Cfg::A_INSTR : 0;
+    constexpr int PARTS = NDMA - DMA0;
+    if constexpr (RESIDENT) {
+      if (nk > 0) {
 #pragma unroll
-      for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
+        for (int s = 0; s < NSTAGE; ++s) {
+          const int k0 = kbeg + s * BK;
+          const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
+#pragma unroll
+          for (int d = DMA0; d < NDMA; ++d) dma_op(s, k0, ra, rb, d);
+        }
+      }
+      // While B's first stages land: the cast of this tile's rows into the resident A stages.
+      if (x_f32) cast_resident(static_cast<const float*>(X));
+      else cast_resident(static_cast<const _Float16*>(X));
+    } else {
+      if (nk > 0) {
+#pragma unroll
+        for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
+      }
     }
-    wait_dma_le<LAG * NDMA>();  // steps 0 and 1 have landed
+    wait_dma_le<LAG * PARTS>();  // steps 0 and 1 have landed
     __syncthreads();
     if (nk > 0) read_frags(0, 0);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -442,18 +566,20 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       constexpr int H = decltype(hc)::value;
       const int kd = kbeg + (j + NSTAGE) * BK;
       const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
+      // resident A: step j+1's own stage (the last step reads an in-range stage it does not use)
+      const int sta = RESIDENT ? (j + 1 < nk ? j + 1 : j) : -1;
       const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
 #pragma unroll
       for (int p = 0; p < PARTS; ++p) {
-        dma_op(std_, kd, ra, rb, p);
+        dma_op(std_, kd, ra, rb, DMA0 + p);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(H, m);
 #pragma unroll
-        for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f);
+        for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f, sta);
         __builtin_amdgcn_sched_barrier(0);
       }
-      wait_dma_le<LAG * NDMA>();  // step j+2 has landed (this wavefront's part)
+      wait_dma_le<LAG * PARTS>();  // step j+2 has landed (this wavefront's part)
       __syncthreads();            // ... every wavefront's part; step j+1 is in registers
     };
     b_run = B + static_cast<size_t>(kbeg + NSTAGE * BK) * N + n0;
@@ -599,7 +725,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
         const int grow = m0 + wm0 + 32 * ri + row;
         const int gcol = n0 + wn0 + 32 * rj + c4;
         if (grow < M && gcol < N) {  // N % 8 == 0: a 4-column chunk is all in or all out
-          const float rs = rscale != nullptr ? rscale[grow] : 1.f;
+          const float rs = RESIDENT ? s_scale[grow - m0] : (rscale != nullptr ? rscale[grow] : 1.f);
           const float4v b = bias != nullptr ? float4v{bias[gcol], bias[gcol + 1], bias[gcol + 2], bias[gcol + 3]}
                                             : float4v{0.f, 0.f, 0.f, 0.f};
           v = v * rs + b;
@@ -716,10 +842,11 @@ KSplit ksplit_for(int K, int ksplit) {
 
 template <bool OUT_F16>
 using GemmFn = void (*)(const _Float16*, const _Float16*, void*, const float*, const float*, float*, uint32_t*, int,
-                        int, int, int, int, int, int);
+                        int, int, int, int, int, int, const void*, int, int);
 
 template <bool OUT_F16>
-GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b) {
+GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b, bool resident = false) {
+  if (resident) return hgemm_kernel<Cfg32, OUT_F16, false, false, false, true>;
   if (packed_b)
     return t == Tile::T256N ? hgemm_kernel<Cfg256n, OUT_F16, false, true, true> : hgemm_kernel<Cfg256, OUT_F16, false, true, true>;
   if (packed) return t == Tile::T256N ? hgemm_kernel<Cfg256n, OUT_F16, false, true> : hgemm_kernel<Cfg256, OUT_F16, false, true>;
@@ -755,17 +882,33 @@ size_t splitk_counter_bytes(const Plan& p, int ksplit) {
 // Launches the GEMM on the tile choose_tile() picks for num_cus compute units (<= 0: the CU count of
 // the stream's device), so that a caller who planned ksplit and sized the split buffers for a CU
 // count gets exactly that grid.
+// The activations of a resident-A launch (mm_t's GEMM path in one launch): X, its type, log2 of
+// the threshold.
+struct ResidentCast {
+  const void* x;
+  int x_f32;
+  int texp;
+};
+
+// mm_t's GEMM path runs as one resident-A launch where the plan is the unsplit 32x128 tile and
+// every K step of A fits in LDS.
+bool resident_route(const Plan& p, int ksplit, int K) {
+  return p.tile == Tile::T32 && ksplit == 1 && K > 0 && ceil_div(K, Cfg32::BK) <= kResidentSteps;
+}
+
 int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, const float* bias, const float* rscale,
                 int M, int N, int K, int ksplit, int num_cus, void* ws, size_t ws_bytes, uint32_t* counters_in,
-                size_t counter_bytes_in, void* stream, bool packed = false, bool packed_b = false) {
+                size_t counter_bytes_in, void* stream, bool packed = false, bool packed_b = false,
+                const ResidentCast* rc = nullptr) {
   if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0 || K > kMaxK || N > kMaxN) return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
   if (ksplit < 1 || ksplit > 256) return G16_E_SPLIT;
-  if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return G16_E_NULL;
+  if (C == nullptr || (K > 0 && ((A == nullptr && rc == nullptr) || B == nullptr))) return G16_E_NULL;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return G16_E_ALIGN;
   const KSplit ks = ksplit_for(K, ksplit);
   if (num_cus <= 0) num_cus = stream_cus(static_cast<hipStream_t>(stream));
   Plan p = choose_tile(M, N, K, num_cus);
+  if (rc != nullptr && !resident_route(p, ks.ksplit, K)) return G16_E_SHAPE;
   if (packed) {
     // the packed layouts are the stage images of the 256-row tiles: the 256x256 tile, or the
     // 256x128 one where the plan picks it
@@ -786,11 +929,14 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   const auto* b = reinterpret_cast<const _Float16*>(B);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool sk = ks.ksplit > 1;
+  const bool res = rc != nullptr;
+  const void* x = res ? rc->x : nullptr;
+  const int x_f32 = res ? rc->x_f32 : 0, texp = res ? rc->texp : 0;
   if (out_f16)
-    return launch(gemm_fn<true>(p.tile, sk, packed, packed_b), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K,
-                  ks.kchunk, ks.ksplit, p.ntm, p.ntn);
-  return launch(gemm_fn<false>(p.tile, sk, packed, packed_b), grid, block, s, a, b, C, bias, rscale, part, counters, M, N, K,
-                ks.kchunk, ks.ksplit, p.ntm, p.ntn);
+    return launch(gemm_fn<true>(p.tile, sk, packed, packed_b, res), grid, block, s, a, b, C, bias, rscale, part, counters,
+                  M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp);
+  return launch(gemm_fn<false>(p.tile, sk, packed, packed_b, res), grid, block, s, a, b, C, bias, rscale, part, counters,
+                M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp);
 }
 
 }  // namespace
@@ -901,8 +1047,20 @@ size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 }  // namespace
 }  // namespace g16
 
+namespace g16 {
+namespace {
+
+bool mm_t_resident(int M, int N, int K, int num_cus) {
+  if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0 || g16_hgemm_use_packed(M, N, K, num_cus) == 1) return false;
+  return resident_route(choose_tile(M, N, K, num_cus), ksplit_for(K, g16_hgemm_plan(M, N, K, num_cus)).ksplit, K);
+}
+
+}  // namespace
+}  // namespace g16
+
 extern "C" size_t g16_mm_t_scratch_bytes(int M, int N, int K, int num_cus) {
   if (M <= 0 || N <= 0 || K < 0) return 0;
+  if (g16::mm_t_resident(M, N, K, num_cus)) return 0;  // one launch; the cast stays in LDS
   const bool packed = g16_hgemm_use_packed(M, N, K, num_cus) == 1;
   return g16::round256(g16::cast_bytes(M, K, packed)) + static_cast<size_t>(M) * sizeof(float);
 }
@@ -916,7 +1074,18 @@ extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, v
   if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0 || K > g16::kMaxK || N > g16::kMaxN || num_cus <= 0)
     return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
-  if (scratch == nullptr || out == nullptr || (K > 0 && (x == nullptr || w_t == nullptr))) return G16_E_NULL;
+  if (out == nullptr || (K > 0 && (x == nullptr || w_t == nullptr))) return G16_E_NULL;
+  if (g16::mm_t_resident(M, N, K, num_cus)) {
+    // one launch: the GEMM's workgroups cast their own rows into LDS (the same bits as the cast
+    // below, the same GEMM arithmetic); no scratch
+    const int texp = g16::thresh_exponent(thresh);
+    if (texp == -1000) return G16_E_SHAPE;
+    if (!g16::aligned16(x)) return G16_E_ALIGN;
+    const g16::ResidentCast rc{x, x_is_f32 != 0 ? 1 : 0, texp};
+    return g16::gemm_launch(nullptr, w_t, out, out_is_f16 != 0, bias, nullptr, M, N, K, 1, num_cus, nullptr, 0, nullptr,
+                            0, stream, false, false, &rc);
+  }
+  if (scratch == nullptr) return G16_E_NULL;
   if (!g16::aligned16(scratch)) return G16_E_ALIGN;
   if (scratch_bytes < g16_mm_t_scratch_bytes(M, N, K, num_cus)) return G16_E_WORKSPACE;
   const bool packed = g16_hgemm_use_packed(M, N, K, num_cus) == 1;

@@ -1,13 +1,8 @@
 // Row rescale + fp16 cast for the quantised GEMM path (M > 8).
 //
-// Semantics (reference: src/gtx16_fp16/kernels.py:227-250, called from ops.py:86-90):
-//   amax_i = max_k |x[i,k]|, starting from 0, NaN ignored;
-//   e_i    = ceil(log2(amax_i / thresh)) if amax_i > thresh else 0;
-//   S_i    = 2^e_i;  y[i,k] = fp16_rne(x[i,k] * 2^-e_i).
-// The exponent is computed from the fp32 bit fields (no log2/exp2): with thresh = 2^t and
-// amax = 1.m * 2^E (normal, since amax > thresh), amax/thresh = 1.m * 2^(E-t), whose ceil(log2)
-// is E - t when the mantissa field is zero and E - t + 1 otherwise. A row with amax = +inf gets
-// S = +inf and y = x * 0.
+// Semantics (reference: src/gtx16_fp16/kernels.py:227-250, called from ops.py:86-90): see
+// rowscale_math.hpp, which holds the arithmetic (shared with the GEMM kernels that cast their own
+// activations).
 //
 // Layout: one 64-lane wavefront per row, 4 rows per 256-thread workgroup. Each lane keeps up to
 // CH 16-byte chunks of its row in registers, so the row is read from HBM once: max-reduce across
@@ -18,66 +13,18 @@
 // packed_offset in g16_common.hpp): every 256-row x 32-column block of y is one contiguous 16 KB
 // run, already in the order (and LDS swizzle) the GEMM's DMA writes into LDS, so that DMA reads
 // whole 1 KB runs instead of 64-byte pieces of 256 different rows.
-#include "g16_common.hpp"
+#include "rowscale_math.hpp"
 
 namespace g16 {
 namespace {
 
 constexpr int kRowsPerBlock = 4;
 
-__device__ inline float chunk_absmax(float m, u32x4 v, float) {
-  m = fmaxf(m, fabsf(__uint_as_float(v.x)));
-  m = fmaxf(m, fabsf(__uint_as_float(v.y)));
-  m = fmaxf(m, fabsf(__uint_as_float(v.z)));
-  m = fmaxf(m, fabsf(__uint_as_float(v.w)));
-  return m;
-}
-
-__device__ inline float lo_h(uint32_t d) { return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(d & 0xffffu))); }
-__device__ inline float hi_h(uint32_t d) { return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(d >> 16))); }
-
-__device__ inline float chunk_absmax(float m, u32x4 v, _Float16) {
-  m = fmaxf(m, fabsf(lo_h(v.x)));
-  m = fmaxf(m, fabsf(hi_h(v.x)));
-  m = fmaxf(m, fabsf(lo_h(v.y)));
-  m = fmaxf(m, fabsf(hi_h(v.y)));
-  m = fmaxf(m, fabsf(lo_h(v.z)));
-  m = fmaxf(m, fabsf(hi_h(v.z)));
-  m = fmaxf(m, fabsf(lo_h(v.w)));
-  m = fmaxf(m, fabsf(hi_h(v.w)));
-  return m;
-}
-
-__device__ inline uint32_t pack2(float a, float b) {
-  const uint16_t lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a));
-  const uint16_t hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(b));
-  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
-}
-
-// x * 2^-e: exact (ldexp keeps the sign of zero and never rounds a product here, since any
-// fp32 result below the normal range is far below half the smallest fp16 subnormal). A row whose
-// scale is +inf (e == kInfExp) maps to x * 0 like the reference's multiply by 1/inf. (A plain
-// multiply by 2^-e is not used: the compiler fuses it with the fp16 conversion into an FMA with a
-// +0 addend, which turns -0 into +0.)
-constexpr int kInfExp = 1 << 20;
-__device__ inline float scale_down(float x, int e) { return e == kInfExp ? x * 0.f : ldexpf(x, -e); }
-
-// fp32 chunk: 4 values -> 4 fp16 (8 bytes).
 __device__ inline void store_scaled(_Float16* y, u32x4 v, int e, float) {
-  u32x2 o;
-  o.x = pack2(scale_down(__uint_as_float(v.x), e), scale_down(__uint_as_float(v.y), e));
-  o.y = pack2(scale_down(__uint_as_float(v.z), e), scale_down(__uint_as_float(v.w), e));
-  *reinterpret_cast<u32x2*>(y) = o;
+  *reinterpret_cast<u32x2*>(y) = cast_scaled(v, e, float{});
 }
-
-// fp16 chunk: 8 values -> 8 fp16 (16 bytes).
 __device__ inline void store_scaled(_Float16* y, u32x4 v, int e, _Float16) {
-  u32x4 o;
-  o.x = pack2(scale_down(lo_h(v.x), e), scale_down(hi_h(v.x), e));
-  o.y = pack2(scale_down(lo_h(v.y), e), scale_down(hi_h(v.y), e));
-  o.z = pack2(scale_down(lo_h(v.z), e), scale_down(hi_h(v.z), e));
-  o.w = pack2(scale_down(lo_h(v.w), e), scale_down(hi_h(v.w), e));
-  *reinterpret_cast<u32x4*>(y) = o;
+  *reinterpret_cast<u32x4*>(y) = cast_scaled(v, e, _Float16{});
 }
 
 // Where input chunk idx of `row` goes: row-major, or tile-packed (an fp32 input chunk is half of
@@ -132,21 +79,9 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const TX* __restrict__ X,
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
 
-  // Exponent from the bit fields; texp is log2(thresh).
-  int e = 0;
-  float sc = 1.f;
-  const uint32_t ab = __float_as_uint(amax);
-  const int E = static_cast<int>((ab >> 23) & 0xffu) - 127;
-  const bool gt = amax > __uint_as_float(static_cast<uint32_t>(texp + 127) << 23);
-  if (gt) {
-    if ((ab & 0x7f800000u) == 0x7f800000u) {  // +inf (NaN never reaches here: fmaxf drops it)
-      sc = __uint_as_float(0x7f800000u);
-      e = kInfExp;
-    } else {
-      e = E - texp + ((ab & 0x007fffffu) != 0u ? 1 : 0);
-      sc = e + 127 >= 255 ? __uint_as_float(0x7f800000u) : __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
-    }
-  }
+  int e;
+  float sc;
+  row_exponent(amax, texp, e, sc);
 
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -156,15 +91,6 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const TX* __restrict__ X,
   for (int idx = lane + CH * kWave; idx < nch; idx += kWave)
     store_scaled(out_at<TX, PACK>(Y, row, K, idx, nks), xr[idx], e, TX{});
   if (lane == 0) S[row] = sc;
-}
-
-// thresh must be a positive, normal power of two; returns its exponent or a sentinel.
-int thresh_exponent(float thresh) {
-  uint32_t b;
-  __builtin_memcpy(&b, &thresh, sizeof(b));
-  const uint32_t ex = (b >> 23) & 0xffu;
-  if ((b >> 31) != 0u || ex == 0u || ex == 0xffu || (b & 0x007fffffu) != 0u) return -1000;
-  return static_cast<int>(ex) - 127;
 }
 
 template <typename TX, int CH, bool PACK>

@@ -189,14 +189,17 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
     # GEMM path: fp16 inputs, with per-row power-of-two scaling for rows that would overflow. One
     # library call runs the rowscale cast into `scratch` and the GEMM on the planned route: the
     # tile-packed 256-row tiles for large outputs, split-K where the tiles leave CUs idle, else the
-    # plain tiles (the cast, scales and GEMM of ops.py:86-108).
+    # plain tiles (the cast, scales and GEMM of ops.py:86-108); on the unsplit 32x128 tile with
+    # K <= 1280 the GEMM casts its own rows into LDS, one launch in all.
     kind, scratch_bytes, _ks, ws_bytes, cnt_bytes = _gemm_route(lib, M, N, K, dev)
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
-    scratch = torch.empty(scratch_bytes, device=dev, dtype=torch.uint8)
+    # no scratch where the GEMM casts its own rows into LDS (one launch, the unsplit small tile)
+    scratch = torch.empty(scratch_bytes, device=dev, dtype=torch.uint8) if scratch_bytes else None
     bufs = split_buffers(dev, stream, ws_bytes, cnt_bytes) if kind == "splitk" else (None, 0, None, 0)
     _clib.check(_clib.fast().mm_t_gemm(x2d.data_ptr(), 1 if x2d.dtype == torch.float32 else 0, w_t.data_ptr(),
                                   out.data_ptr(), 1 if out_dtype == torch.float16 else 0, bptr, ROW_SCALE_THRESHOLD,
-                                  M, N, K, _sm_count(dev), scratch.data_ptr(), scratch_bytes, *bufs, stream), "GEMM")
+                                  M, N, K, _sm_count(dev), None if scratch is None else scratch.data_ptr(),
+                                  scratch_bytes, *bufs, stream), "GEMM")
     return out
 
 

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 11
+#define G16_ABI_VERSION 12
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -123,9 +123,13 @@ int g16_hgemm_use_packed(int M, int N, int K, int num_cus);
  * mm_t's GEMM path (src/gtx16_fp16/ops.py:86-108) in one call: the rowscale cast of x (fp32 when
  * x_is_f32, else fp16) into `scratch`, then the GEMM on the route this library plans for num_cus
  * compute units -- the tile-packed route where g16_hgemm_use_packed() is 1, else split-K with
- * ksplit = g16_hgemm_plan() when that is > 1, else the plain GEMM. The same two launches, and the
- * same result bits, as the separate entry points; one call instead of two on a path whose small
- * shapes are bound by host time. No counterpart kernel in the reference.
+ * ksplit = g16_hgemm_plan() when that is > 1, else the plain GEMM. The same result bits as the
+ * separate entry points (rowscale, then GEMM); one call instead of two on a path whose small
+ * shapes are bound by host and launch time. No counterpart kernel in the reference.
+ *   One launch: where the plan is the unsplit 32x128 tile and K <= 1280, the GEMM's workgroups
+ *   cast their own rows of x into LDS (the rowscale arithmetic, the same bits) and no rowscale
+ *   launch runs; g16_mm_t_scratch_bytes() is then 0 and scratch may be NULL (x must be 16-byte
+ *   aligned). Elsewhere the call makes the two launches.
  *   scratch: at least g16_mm_t_scratch_bytes(M, N, K, num_cus) bytes, 16-byte aligned (the fp16
  *   cast and the row scales; it must stay allocated until the GEMM has run).
  *   workspace / counters: as g16_hgemm_splitk needs them for that ksplit (unused otherwise, then

@@ -52,12 +52,17 @@ def test_argument_errors_need_no_gpu(lib):
     assert lib.g16_skinny_f32in(A, A, A + 4, None, 1, 64, 64, 1, None, 0, None, 0, None) == -2  # C alignment
     # split partials beyond a 2 GiB workspace (8 x 65536 x 1024 slices x 4 bytes) are refused
     assert lib.g16_skinny_f32in(A, A, A, None, 8, 65536, 8192, 1024, A, 1 << 40, A, 1 << 20, None) == -5
-    need = lib.g16_mm_t_scratch_bytes(64, 64, 64, 256)
-    assert need == 64 * 64 * 2 + 64 * 4                                        # cast + row scales
-    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A, need - 1, None, 0, None, 0, None) == -4
-    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A + 8, need, None, 0, None, 0, None) == -2
-    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 64, 256, A, need, None, 0, None, 0, None) == -1
-    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 64, 256, A, need, None, 0, None, 0, None) == 0
+    need = lib.g16_mm_t_scratch_bytes(64, 64, 2048, 256)
+    assert need == 64 * 2048 * 2 + 64 * 4                                      # cast + row scales
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 2048, 256, A, need - 1, None, 0, None, 0, None) == -4
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 2048, 256, A + 8, need, None, 0, None, 0, None) == -2
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 2048, 256, A, need, None, 0, None, 0, None) == -1
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 2048, 256, A, need, None, 0, None, 0, None) == 0
+    # the one-launch route (no scratch): misaligned x and a threshold that is not 2^k are refused
+    assert lib.g16_mm_t_scratch_bytes(64, 64, 64, 256) == 0
+    assert lib.g16_mm_t_gemm(A + 4, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, None, 0, None, 0, None, 0, None) == -2
+    assert lib.g16_mm_t_gemm(A, 1, A, A, 0, None, 1000.0, 64, 64, 64, 256, None, 0, None, 0, None, 0, None) == -1
+    assert lib.g16_mm_t_gemm(A, 1, A, None, 0, None, 1024.0, 64, 64, 64, 256, None, 0, None, 0, None, 0, None) == -3
     # the no-allocation skinny variant refuses splits past its static scratch before any HIP call:
     # 32 slices x 8 x 16384 x 4 bytes = 16 MiB of partials > 4 MiB; N = 131080 needs 257 counter lines
     assert lib.g16_skinny_f32in_noalloc(A, A, A, None, 8, 16384, 4096, 32, None) == -7
@@ -150,6 +155,15 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_hgemm_splitk_counter_bytes(64, 1024, 1024, 4, 0) > 0
 
 
+def test_one_launch_route_needs_no_scratch(lib):
+    # mm_t's GEMM path is one launch (the cast in LDS, no scratch) exactly where the plan is the
+    # unsplit 32x128 tile and K <= 1280
+    for M, N, K in [(1024, 1024, 1024), (1000, 1000, 1000), (1024, 1024, 1280), (20, 1024, 256), (1000, 1024, 8)]:
+        assert lib.g16_mm_t_scratch_bytes(M, N, K, 256) == 0, (M, N, K)
+    for M, N, K in [(1024, 1024, 1288), (1024, 1024, 2048), (20, 1024, 512), (64, 1024, 1024), (4096, 4096, 4096)]:
+        assert lib.g16_mm_t_scratch_bytes(M, N, K, 256) > 0, (M, N, K)
+
+
 def test_fast_extension_matches_the_c_entry_points(lib):
     # _g16fast forwards its arguments unchanged: the same rejected calls give the same statuses
     fast = _clib.fast()
@@ -158,12 +172,12 @@ def test_fast_extension_matches_the_c_entry_points(lib):
     assert fast.skinny_f32in(A, A, A + 4, None, 1, 64, 64, 1, None, 0, None, 0, None) == -2
     assert fast.skinny_f32in(A, A, A, None, 4, 4096, 4096, 8, A, 1 << 30, None, 0, None) == -4
     assert fast.skinny_f32in(A, A, A, None, 8, 65536, 8192, 1024, A, 1 << 40, A, 1 << 20, None) == -5
-    need = lib.g16_mm_t_scratch_bytes(64, 64, 64, 256)
-    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A, need - 1, None, 0, None, 0, None) == -4
-    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 64, 256, A + 8, need, None, 0, None, 0, None) == -2
-    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 64, 256, A, need, None, 0, None, 0, None) == -1
-    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1000.0, 64, 64, 64, 256, A, need, None, 0, None, 0, None) == -1
-    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 64, 256, A, need, None, 0, None, 0, None) == 0
+    need = lib.g16_mm_t_scratch_bytes(64, 64, 2048, 256)
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 2048, 256, A, need - 1, None, 0, None, 0, None) == -4
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 64, 2048, 256, A + 8, need, None, 0, None, 0, None) == -2
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 2048, 256, A, need, None, 0, None, 0, None) == -1
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1000.0, 64, 64, 64, 256, None, 0, None, 0, None, 0, None) == -1
+    assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 2048, 256, A, need, None, 0, None, 0, None) == 0
     with pytest.raises(TypeError):
         fast.skinny_f32in(A, A, A)
     with pytest.raises(OverflowError):
