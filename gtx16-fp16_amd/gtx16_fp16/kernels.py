@@ -86,9 +86,16 @@ class PreparedLaunch:
 _ws_lock = threading.Lock()
 _partials: dict[tuple[int, int], torch.Tensor] = {}
 _counters: dict[tuple[int, int], torch.Tensor] = {}
+_scratch: dict[tuple[int, int], torch.Tensor] = {}
 _retired: list[torch.Tensor] = []
+# (device index, stream) -> (partial bytes, counter bytes, the pointer tuple split_buffers returns):
+# the per-call lookup of a stream whose buffers are already large enough
+_current: dict[tuple[int, int], tuple] = {}
 _MIN_PARTIAL_BYTES = 1 << 20
 _MIN_COUNTER_BYTES = 64 << 10
+# mm_t's cast scratch is kept per stream up to this size (small GEMMs are bound by host time, and
+# an allocation is ~1.3 us of it); larger casts are allocated per call like the reference's
+_MAX_CACHED_SCRATCH = 16 << 20
 
 
 def _grown(table: dict, key, nbytes: int, floor: int, device, zero: bool) -> torch.Tensor:
@@ -113,9 +120,28 @@ def split_buffers(device: torch.device, stream: int, partial_bytes: int, counter
     if partial_bytes <= 0 and counter_bytes <= 0:
         return 0, 0, 0, 0
     key = (device.index or 0, stream)
+    hit = _current.get(key)
+    if hit is not None and hit[0] >= partial_bytes and hit[1] >= counter_bytes:
+        return hit[2]
     part = _grown(_partials, key, partial_bytes, _MIN_PARTIAL_BYTES, device, zero=False)
     cnt = _grown(_counters, key, counter_bytes, _MIN_COUNTER_BYTES, device, zero=True)
-    return part.data_ptr(), part.numel(), cnt.data_ptr(), cnt.numel()
+    ptrs = (part.data_ptr(), part.numel(), cnt.data_ptr(), cnt.numel())
+    _current[key] = (part.numel(), cnt.numel(), ptrs)
+    return ptrs
+
+
+def scratch_buffer(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """A uint8 device buffer of at least ``nbytes`` for the cast of one mm_t call on ``stream``:
+    kept per (device, stream) and reused by the next call there (calls on one stream are ordered)
+    up to 16 MiB; above that a fresh allocation per call. A buffer that is outgrown stays alive,
+    like the split buffers, since a captured graph may still use it."""
+    if nbytes > _MAX_CACHED_SCRATCH:
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device.index or 0, stream)
+    buf = _scratch.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = _grown(_scratch, key, nbytes, 1 << 20, device, zero=False)
+    return buf
 
 
 def release_workspaces() -> None:
@@ -124,4 +150,6 @@ def release_workspaces() -> None:
     with _ws_lock:
         _partials.clear()
         _counters.clear()
+        _scratch.clear()
+        _current.clear()
         _retired.clear()

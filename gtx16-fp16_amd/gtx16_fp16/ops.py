@@ -10,7 +10,7 @@ import weakref
 import torch
 
 from . import _clib
-from .kernels import SKINNY_MAX_M, split_buffers, stream_handle
+from .kernels import SKINNY_MAX_M, scratch_buffer, split_buffers, stream_handle
 
 # ops.py:14-16 -- rows whose |max| exceeds this are scaled down by a power of two before the fp16
 # cast (GEMM path); the result is scaled back in fp32.
@@ -194,7 +194,7 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
     kind, scratch_bytes, _ks, ws_bytes, cnt_bytes = _gemm_route(lib, M, N, K, dev)
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
     # no scratch where the GEMM casts its own rows into LDS (one launch, the unsplit small tile)
-    scratch = torch.empty(scratch_bytes, device=dev, dtype=torch.uint8) if scratch_bytes else None
+    scratch = scratch_buffer(dev, stream, scratch_bytes) if scratch_bytes else None
     bufs = split_buffers(dev, stream, ws_bytes, cnt_bytes) if kind == "splitk" else (None, 0, None, 0)
     _clib.check(_clib.fast().mm_t_gemm(x2d.data_ptr(), 1 if x2d.dtype == torch.float32 else 0, w_t.data_ptr(),
                                   out.data_ptr(), 1 if out_dtype == torch.float16 else 0, bptr, ROW_SCALE_THRESHOLD,

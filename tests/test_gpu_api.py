@@ -208,6 +208,47 @@ def test_graph_capture_replays_match_eager(g, cuda):
                 assert torch.equal(fl(x), eager)
 
 
+def test_graphs_of_mm_t_keep_their_buffers_when_a_later_capture_outgrows_them(g, cuda):
+    # mm_t keeps its cast scratch and split buffers per stream and grows them on demand; a graph
+    # captured before a larger capture on the same stream must keep replaying correctly (the
+    # outgrown buffers stay alive and are never handed to anything else).
+    small = [(64, 1024, 1024), (100, 2048, 520)]          # split-K route; plain route with a cast
+    large = [(64, 4096, 11008), (1536, 4096, 1024)]      # more partials; a larger cast
+    s = torch.cuda.Stream(cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+
+    def capture(shapes, seed):
+        xs = [torch.randn(M, K, device=cuda, generator=torch.Generator(cuda).manual_seed(seed + i))
+              for i, (M, K, N) in enumerate(shapes)]
+        ws = [(torch.randn(K, N, device=cuda, generator=torch.Generator(cuda).manual_seed(seed + 9 + i)) * 0.02).half()
+              for i, (M, K, N) in enumerate(shapes)]
+        with torch.cuda.stream(s):
+            for x, w in zip(xs, ws):
+                g.mm_t(x, w)  # eager on the capture stream first: its buffers exist
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=s):
+                outs = [g.mm_t(x, w) for x, w in zip(xs, ws)]
+        torch.cuda.current_stream(cuda).wait_stream(s)
+        torch.cuda.synchronize()
+        eager = [g.mm_t(x, w) for x, w in zip(xs, ws)]
+        return graph, outs, eager, (xs, ws)  # the graph reads xs and ws: keep them alive
+
+    g1, outs1, eager1, keep1 = capture(small, 100)
+    g2, outs2, eager2, keep2 = capture(large, 200)
+    for _ in range(3):
+        for o in outs1 + outs2:
+            o.fill_(0.0)
+        g1.replay()
+        g2.replay()
+        g1.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs1, eager1):
+            assert torch.equal(o, e)
+        for o, e in zip(outs2, eager2):
+            assert torch.equal(o, e)
+
+
 def test_gemm_clock_stamps_give_a_plausible_clock(cuda):
     # g16_gemm_clock: workgroup 0's main-loop shader cycles and 100 MHz ticks of the latest GEMM
     from gtx16_fp16 import _clib
