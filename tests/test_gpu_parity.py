@@ -317,8 +317,11 @@ def test_small_tiles_odd_and_even_step_counts(lib, cuda, M, N, bk, num_cus, tile
 # skinny path (M <= 8)
 # ---------------------------------------------------------------------------------------------
 
+# 256-column strips up to N = 8192, 512-column strips above (8200: one 8-column group past 16
+# strips; 11008 and 14336: the LLM MLP widths)
 SKINNY_SHAPES = [(1, 4096, 4096), (4, 4096, 4096), (1, 1024, 3072), (8, 2048, 520), (3, 4096, 4096),
-                 (2, 8, 8), (5, 200, 72), (7, 1032, 776), (6, 64, 4104)]
+                 (2, 8, 8), (5, 200, 72), (7, 1032, 776), (6, 64, 4104), (1, 1000, 8192), (2, 520, 8200),
+                 (1, 4096, 11008), (8, 1024, 14336), (4, 4096, 14336), (6, 136, 9000)]
 
 
 @pytest.mark.parametrize("M,K,N", SKINNY_SHAPES)
@@ -505,16 +508,20 @@ def test_packed_gemm_bitwise_equals_rowmajor(lib, cuda, M, K, N, out_dtype):
     assert oracle.rel_err(_np(c_pk.float()), ref.astype(np.float64)) <= GEMM_TOL
 
 
-@pytest.mark.parametrize("M", [1, 4])
-def test_skinny_partial_block_ignores_rows_past_the_slice(lib, cuda, M):
-    # K=1024 with ksplit 16 gives each wavefront 8 rows, fewer than it loads at once: the last block
-    # re-reads the slice's last row for the missing ones and must not use them. A +inf in that last
-    # row must therefore reach the output as +inf (a 0 * inf from a reused row would make it NaN).
-    K, N, ksplit = 1024, 1024, 16
+# (M, K, N, ksplit, rows per wavefront), each with fewer rows per wavefront than its batch: 256-column
+# strips (two rows per load instruction; 8-row batches for M = 1 and 4, 16-row ones for M = 5) and
+# the 512-column strips of N > 8192 (8-row batches for M = 1, 16-row ones for M = 8)
+@pytest.mark.parametrize("M,K,N,ksplit,rpw", [(1, 1024, 1024, 32, 4), (4, 1024, 1024, 32, 4),
+                                              (5, 1024, 1024, 16, 8), (1, 1024, 8704, 32, 4),
+                                              (8, 1024, 8704, 16, 8)])
+def test_skinny_partial_block_ignores_rows_past_the_slice(lib, cuda, M, K, N, ksplit, rpw):
+    # A wavefront with fewer rows than its batch loads: the last batch re-reads the slice's last row
+    # for the missing ones and must not use them. A +inf in that last row must therefore reach the
+    # output as +inf (a 0 * inf from a reused row would make it NaN).
     x = randn((M, K), seed=21).abs() + 0.5          # positive activations
     w = randn((K, N), seed=22, scale=0.02, dtype=torch.float16)
-    w[7, 5] = float("inf")                          # last row of wavefront 0 of slice 0
-    w[1023, 9] = float("inf")                       # last row of the last slice
+    w[rpw - 1, 5] = float("inf")                    # last row of wavefront 0 of slice 0
+    w[K - 1, 9] = float("inf")                      # last row of the last slice
     xd, wd = x.to(cuda), w.to(cuda)
     out = torch.empty(M, N, device=cuda)
     st = _stream(cuda)
