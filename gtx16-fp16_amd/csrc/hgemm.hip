@@ -40,6 +40,14 @@
 //     row's scale (rowscale_math.hpp, the rowscale kernel's arithmetic) and writes the scaled fp16
 //     rows into LDS as the stage images of every K step, which then stay resident; only B streams
 //     through the ring. No fp16 copy of A goes to HBM and no separate rowscale launch runs.
+//   * Speculative fp16 A (the 4-wavefront tiles with fp16 activations, mm_t's GEMM path in one
+//     launch): a row whose |max| does not exceed the threshold has scale 1, and its rowscale cast is
+//     the activation itself. So the GEMM streams x as A and tracks the largest |x| it multiplies
+//     (from the A fragments). If no row of the tile exceeds the threshold, the result is the cast
+//     path's, bit for bit. Otherwise the tile is computed again from the rescaled cast: unsplit
+//     tiles right away (cast into LDS for the resident tile, else into the scratch buffer), split
+//     tiles by the slice that arrives last (every flagged slice marks the arrival count), which
+//     recomputes every slice in slice order -- the same sums the split reduction adds.
 //   * Split-K: slice z of tile t covers K range [z*kchunk, (z+1)*kchunk). Every slice stores its
 //     fp32 accumulators to the workspace in the lanes' own register order (fully coalesced 16-byte
 //     device-coherent stores); the last slice to arrive adds all slices in slice order and runs the
@@ -58,6 +66,9 @@ constexpr int kSplitAlign = 64;  // split-K slices start on a multiple of every 
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every descriptor's range: reads 0
 
 typedef short short4v __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2v __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x4v __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) short4v lds_short4v;
 
@@ -181,6 +192,22 @@ __device__ inline float wave_max(float v) {
   return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// arrive_last_coherent with a value: every thread of the workgroup calls it after its coherent
+// stores; the workgroup adds `add` to the counter and every thread gets the counter's value after
+// that addition.
+__device__ inline uint32_t arrive_add_coherent(uint32_t* counter, uint32_t add) {
+  __shared__ uint32_t s_val;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed at the coherence point
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) s_val = __hip_atomic_fetch_add(counter, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+  __syncthreads();
+  return s_val;
+}
+// A speculative slice whose A exceeded the threshold adds this on top of its arrival.
+constexpr uint32_t kSpecFlag = 1u << 16;
+
 // Workgroup barrier without the counter waits __syncthreads() adds: the caller has already waited
 // for exactly the memory operations the next phase depends on. The memory clobber keeps the
 // compiler from moving LDS accesses across it.
@@ -188,21 +215,27 @@ __device__ inline void phase_barrier() { asm volatile("s_barrier" ::: "memory");
 
 // RESIDENT: A is unused; the kernel casts X (fp32 when x_f32, else fp16; threshold 2^texp) itself
 // into resident LDS stages (the 32x128 tile, unsplit, K <= kResidentSteps * BK).
-template <class Cfg, bool OUT_F16, bool SPLITK, bool PACKED_A = false, bool PACKED_B = false, bool RESIDENT = false>
+// SPEC: A (and X) are the fp16 activations, streamed as they are; tbits is the largest fp16 bit
+// pattern not above the threshold. A tile with a larger |x| is recomputed from the rescaled cast:
+// in the resident LDS stages (with RESIDENT) or in ys (row-major, M x K fp16).
+template <class Cfg, bool OUT_F16, bool SPLITK, bool PACKED_A = false, bool PACKED_B = false, bool RESIDENT = false,
+          bool SPEC = false>
 __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
                                                          void* __restrict__ Cv, const float* __restrict__ bias,
                                                          const float* __restrict__ rscale, float* __restrict__ part,
                                                          uint32_t* __restrict__ counters, int M, int N, int K,
                                                          int kchunk, int ksplit, int ntm, int ntn,
-                                                         const void* __restrict__ X, int x_f32, int texp) {
+                                                         const void* __restrict__ X, int x_f32, int texp,
+                                                         _Float16* __restrict__ ys, int tbits) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN, MB = Cfg::MB, MK = Cfg::MK;
   constexpr int BK = Cfg::BK, NSTAGE = Cfg::NSTAGE;
   static_assert(!RESIDENT || (Cfg::BM == 32 && Cfg::BK == 64 && Cfg::WAVES == 4 && !SPLITK && !PACKED_A && !PACKED_B),
                 "resident A: the unsplit 32x128 tile");
+  static_assert(!SPEC || (Cfg::WAVES == 4 && !Cfg::MF16 && !PACKED_A && !PACKED_B), "speculative A: the 4-wavefront tiles");
   constexpr int A_STAGES = RESIDENT ? kResidentSteps : NSTAGE;
   __shared__ __attribute__((aligned(1024))) unsigned char sA[A_STAGES][Cfg::A_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char sB[NSTAGE][Cfg::B_BYTES];
-  __shared__ float s_scale[RESIDENT ? BM : 1];
+  __shared__ float s_scale[(RESIDENT || SPEC) ? BM : 1];
   const uint32_t sA_lds = lds_base(&sA[0][0]), sB_lds = lds_base(&sB[0][0]);
 
   // ---- tile assignment (XCD-aware, grouped) ----
@@ -217,9 +250,10 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   const int tile = tm * ntn + tn;
   const int m0 = tm * BM, n0 = tn * BN;
   const int z = blockIdx.y;
-  const int kbeg = z * kchunk;
-  const int kend = min(K, kbeg + kchunk);
-  const int nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
+  // this slice's K range (the speculative path's recomputation walks every slice's range)
+  int kbeg = z * kchunk;
+  int kend = min(K, kbeg + kchunk);
+  int nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -241,6 +275,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // DMA of K step k0 into stage `st`, one 1 KB instruction at a time (instruction d < A_INSTR: A,
   // else B). Steps past the slice are all out of range (zeros, no traffic): they keep the number
   // of DMA operations per step constant, which the vmcnt waits rely on.
+  const _Float16* a_src = A;  // row-major A: the activations, or the speculative path's rescaled cast
   auto rsrc_a = [&](int k0) {
     if constexpr (PACKED_A) {
       static_assert(Cfg::BM == 256 && Cfg::BK == 32 && !SPLITK, "packed A is the stage image of 256 rows x 32 K");
@@ -248,7 +283,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
           const_cast<_Float16*>(A) + static_cast<size_t>(tm) * ceil_div(K, BK) * (Cfg::A_BYTES / 2), 0, 0x7fffffff,
           kRawBufferDword3);
     } else {
-      return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A) + static_cast<size_t>(m0) * K + k0, 0,
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a_src) + static_cast<size_t>(m0) * K + k0, 0,
                                                0x7fffffff, kRawBufferDword3);
     }
   };
@@ -357,6 +392,26 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // of step j run on set j&1 while the LDS reads of step j+1 fill set (j+1)&1.
   constexpr int KS = BK / MK;
   half8 af[2][KS][TM], bf[2][KS][TN];
+  // Speculative A: the largest |x| this lane has multiplied, per fp16 half of a dword, as the bit
+  // pattern shifted left by one (the shift drops the sign; fp16 magnitudes order like their bits;
+  // a NaN counts as large, which only costs a recompute).
+  u16x2v amax_pk = {0, 0};
+  auto track_amax = [&](int buf) {
+    if constexpr (SPEC) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          // Whole-vector shuffles only: hipcc lowers __builtin_bit_cast of one element of a
+          // vector (u.y) as a read of element 0, so such a form would see 2 of every 8 halves.
+          const u16x8v u = __builtin_bit_cast(u16x8v, af[buf][ks][i]) << static_cast<unsigned short>(1);
+          const u16x4v q = __builtin_elementwise_max(__builtin_shufflevector(u, u, 0, 1, 2, 3),
+                                                     __builtin_shufflevector(u, u, 4, 5, 6, 7));
+          amax_pk = __builtin_elementwise_max(
+              amax_pk, __builtin_elementwise_max(__builtin_shufflevector(q, q, 0, 1), __builtin_shufflevector(q, q, 2, 3)));
+        }
+    }
+  };
   // fragment read f of a step: f = ks * (TM + TN) + (i < TM ? i : TM + j)
   // st: the ring stage of B (and of A); sta: A's stage where it differs (the resident-A tile keeps
   // every K step's A image in its own stage)
@@ -470,6 +525,80 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
 
   static_assert(NSTAGE >= 3, "three stages at least");
   constexpr int NMFMA = KS * TM * TN, NFRAG = KS * (TM + TN), NDMA = Cfg::DMA_PER_STEP;
+  // ---- 4-wavefront tiles: a ring of NSTAGE stages ----
+  // During step j: MFMAs of step j (its fragments are already in registers, read during step j-1),
+  // LDS reads of step j+1, and DMA of step j+NSTAGE into stage j%NSTAGE -- the stage step j came
+  // from, which nobody reads any more. Before the barrier that ends step j, step j+2 must have
+  // landed (it is read during j+1): NSTAGE-2 younger steps of DMA may still be in flight, giving
+  // each DMA NSTAGE-1 steps to arrive. The three streams are cut into PARTS slices issued
+  // round-robin (DMA, MFMAs, LDS reads), so no wavefront front-loads its DMA and the memory pipes
+  // see a steady trickle between barriers.
+  constexpr int LAG = NSTAGE - 2;
+  // One pass of the K loop over [kbeg, kend) into acc, with A streamed through the ring (RES
+  // false) or cast into the resident stages first (RES true).
+  auto kloop4 = [&](auto resc) {
+    constexpr bool RES = decltype(resc)::value;
+    // DMA instructions per step: A and B, or B alone with resident A
+    constexpr int DMA0 = RES ? Cfg::A_INSTR : 0;
+    constexpr int PARTS = NDMA - DMA0;
+    if constexpr (RES) {
+      if (nk > 0) {
+#pragma unroll
+        for (int s = 0; s < NSTAGE; ++s) {
+          const int k0 = kbeg + s * BK;
+          const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
+#pragma unroll
+          for (int d = DMA0; d < NDMA; ++d) dma_op(s, k0, ra, rb, d);
+        }
+      }
+      // While B's first stages land: the cast of this tile's rows into the resident A stages.
+      if (x_f32) cast_resident(static_cast<const float*>(X));
+      else cast_resident(static_cast<const _Float16*>(X));
+    } else {
+      if (nk > 0) {
+#pragma unroll
+        for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
+      }
+    }
+    wait_dma_le<LAG * PARTS>();  // steps 0 and 1 have landed
+    __syncthreads();
+    if (nk > 0) read_frags(0, 0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();  // every wavefront holds step 0 in registers: stage 0 may be refilled
+    // Step j on fragment buffer H (a compile-time constant, so two steps make one loop trip). The
+    // loop body has no branches: a conditional step or a conditional read inside it made the
+    // compiler copy accumulators between AGPRs and VGPRs on every trip (measured: ~3x slower
+    // steps). The last step's reads of step j+1 are harmless: they read a stage inside the ring
+    // (zeros or stale data) into the buffer no MFMA uses afterwards.
+    auto step = [&](auto hc, int j) {
+      constexpr int H = decltype(hc)::value;
+      const int kd = kbeg + (j + NSTAGE) * BK;
+      const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
+      // resident A: step j+1's own stage (the last step reads an in-range stage it does not use)
+      const int sta = RES ? (j + 1 < nk ? j + 1 : j) : -1;
+      const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
+      if constexpr (SPEC && !RES) track_amax(H);  // step j's A fragments (streamed x)
+#pragma unroll
+      for (int p = 0; p < PARTS; ++p) {
+        dma_op(std_, kd, ra, rb, DMA0 + p);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(H, m);
+#pragma unroll
+        for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f, sta);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_dma_le<LAG * PARTS>();  // step j+2 has landed (this wavefront's part)
+      __syncthreads();            // ... every wavefront's part; step j+1 is in registers
+    };
+    b_run = B + static_cast<size_t>(kbeg + NSTAGE * BK) * N + n0;
+    int it = 0;
+    for (; it + 1 < nk; it += 2) {
+      step(std::integral_constant<int, 0>{}, it);
+      step(std::integral_constant<int, 1>{}, it + 1);
+    }
+    if (it < nk) step(std::integral_constant<int, 0>{}, it);
+  };
   if constexpr (Cfg::WAVES == 8) {
     // Ping-pong schedule for two wavefronts per SIMD. Wavefronts 0-3 (group 0) and 4-7 (group 1)
     // land one of each on every SIMD. Each wavefront alternates a memory phase M_j (fragment reads
@@ -522,78 +651,64 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     }
     if (grp == 0) phase_barrier();  // every wavefront passes the same number of barriers
   } else {
-    // Ring of NSTAGE stages. During step j: MFMAs of step j (its fragments are already in
-    // registers, read during step j-1), LDS reads of step j+1, and DMA of step j+NSTAGE into
-    // stage j%NSTAGE -- the stage step j came from, which nobody reads any more. Before the
-    // barrier that ends step j, step j+2 must have landed (it is read during j+1): NSTAGE-2
-    // younger steps of DMA may still be in flight, giving each DMA NSTAGE-1 steps to arrive.
-    // The three streams are cut into PARTS slices issued round-robin (DMA, MFMAs, LDS reads), so
-    // no wavefront front-loads its DMA and the memory pipes see a steady trickle between barriers.
-    constexpr int LAG = NSTAGE - 2;
-    // DMA instructions per step: A and B, or B alone with resident A
-    constexpr int DMA0 = RESIDENT ? Cfg::A_INSTR : 0;
-    constexpr int PARTS = NDMA - DMA0;
-    if constexpr (RESIDENT) {
-      if (nk > 0) {
-#pragma unroll
-        for (int s = 0; s < NSTAGE; ++s) {
-          const int k0 = kbeg + s * BK;
-          const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
-#pragma unroll
-          for (int d = DMA0; d < NDMA; ++d) dma_op(s, k0, ra, rb, d);
-        }
-      }
-      // While B's first stages land: the cast of this tile's rows into the resident A stages.
-      if (x_f32) cast_resident(static_cast<const float*>(X));
-      else cast_resident(static_cast<const _Float16*>(X));
-    } else {
-      if (nk > 0) {
-#pragma unroll
-        for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
-      }
-    }
-    wait_dma_le<LAG * PARTS>();  // steps 0 and 1 have landed
-    __syncthreads();
-    if (nk > 0) read_frags(0, 0);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __syncthreads();  // every wavefront holds step 0 in registers: stage 0 may be refilled
-    // Step j on fragment buffer H (a compile-time constant, so two steps make one loop trip). The
-    // loop body has no branches: a conditional step or a conditional read inside it made the
-    // compiler copy accumulators between AGPRs and VGPRs on every trip (measured: ~3x slower
-    // steps). The last step's reads of step j+1 are harmless: they read a stage inside the ring
-    // (zeros or stale data) into the buffer no MFMA uses afterwards.
-    auto step = [&](auto hc, int j) {
-      constexpr int H = decltype(hc)::value;
-      const int kd = kbeg + (j + NSTAGE) * BK;
-      const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
-      // resident A: step j+1's own stage (the last step reads an in-range stage it does not use)
-      const int sta = RESIDENT ? (j + 1 < nk ? j + 1 : j) : -1;
-      const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
-#pragma unroll
-      for (int p = 0; p < PARTS; ++p) {
-        dma_op(std_, kd, ra, rb, DMA0 + p);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(H, m);
-#pragma unroll
-        for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f, sta);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      wait_dma_le<LAG * PARTS>();  // step j+2 has landed (this wavefront's part)
-      __syncthreads();            // ... every wavefront's part; step j+1 is in registers
-    };
-    b_run = B + static_cast<size_t>(kbeg + NSTAGE * BK) * N + n0;
-    int it = 0;
-    for (; it + 1 < nk; it += 2) {
-      step(std::integral_constant<int, 0>{}, it);
-      step(std::integral_constant<int, 1>{}, it + 1);
-    }
-    if (it < nk) step(std::integral_constant<int, 0>{}, it);
+    if constexpr (RESIDENT && !SPEC) kloop4(std::true_type{});
+    else kloop4(std::false_type{});
   }
   wait_dma_le<0>();  // no DMA may still be writing LDS past this point
   if (stamps && tid == 0) {
     g_loop_clock[0] = __builtin_amdgcn_s_memtime() - clk_c0;
     g_loop_clock[1] = __builtin_amdgcn_s_memrealtime() - clk_r0;
+  }
+
+  // ---- speculative A: recompute from the rescaled cast where some |x| exceeded the threshold ----
+  bool respec = false;  // acc comes from the rescaled cast, with the row scales in s_scale
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
+  };
+  // This tile's rows of x over all of K, cast as the rowscale kernel casts them (same arithmetic)
+  // into ys, their scales into s_scale; one wavefront per row. Other workgroups of the tile row
+  // may write the same rows at the same time, with the same bits.
+  auto cast_rows_to_ys = [&]() {
+    if constexpr (SPEC) {
+      const int rows = min(BM, M - m0);
+      const int nch = K / 8;
+      for (int r = wave; r < rows; r += Cfg::WAVES) {
+        const u32x4* xr = reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m0 + r) * K);
+        float am = 0.f;
+        for (int idx = lane; idx < nch; idx += kWave) am = chunk_absmax(am, xr[idx], _Float16{});
+        am = wave_max(am);
+        int e;
+        float sc;
+        row_exponent(am, texp, e, sc);
+        if (lane == 0) s_scale[r] = sc;
+        u32x4* yr = reinterpret_cast<u32x4*>(ys + static_cast<size_t>(m0 + r) * K);
+        for (int idx = lane; idx < nch; idx += kWave) yr[idx] = cast_scaled(xr[idx], e, _Float16{});
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // the cast is in L2 before this workgroup's DMA reads it
+      __syncthreads();
+    }
+  };
+  int over = 0;  // some |x| of this slice exceeded the threshold (the whole workgroup agrees)
+  if constexpr (SPEC) {
+    const uint32_t lane_max = amax_pk.x > amax_pk.y ? amax_pk.x : amax_pk.y;
+    over = __syncthreads_or(lane_max > (static_cast<uint32_t>(tbits) << 1) ? 1 : 0);
+  }
+  if constexpr (SPEC && !SPLITK) {
+    if (over) {
+      respec = true;
+      zero_acc();
+      if constexpr (RESIDENT) {
+        kloop4(std::true_type{});  // cast into the resident stages (and s_scale), then the K loop
+      } else {
+        cast_rows_to_ys();
+        a_src = ys;
+        kloop4(std::false_type{});
+      }
+      wait_dma_le<0>();
+    }
   }
 
   // ---- split-K: publish this slice, let the last slice reduce ----
@@ -631,10 +746,39 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     };
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) store_coherent4(slices, slot_off(z, s), piece(s));
-    if (!arrive_last_coherent(counters + tile * kCounterStride, static_cast<uint32_t>(ksplit))) return;
+    if constexpr (SPEC) {
+      const uint32_t total = arrive_add_coherent(counters + tile * kCounterStride, over ? 1u + kSpecFlag : 1u);
+      if ((total & (kSpecFlag - 1u)) != static_cast<uint32_t>(ksplit)) return;
+      respec = total >= kSpecFlag;
+    } else {
+      if (!arrive_last_coherent(counters + tile * kCounterStride, static_cast<uint32_t>(ksplit))) return;
+    }
     // Slices are added in slice order (every slice, this one's included, is read back from the
     // workspace), so each output is the same sum whichever slice arrives last.
-    if constexpr (SLOTS <= 16) {
+    if (SPEC && respec) {
+      // Some slice's A exceeded the threshold: recompute every slice from the rescaled cast and add
+      // them in slice order, exactly as the reduction below adds the published slices.
+      if constexpr (SPEC) {
+        static_assert(SLOTS <= 16, "the 4-wavefront tiles");
+        cast_rows_to_ys();
+        a_src = ys;
+        float4v sum[SLOTS];
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
+        for (int zz = 0; zz < ksplit; ++zz) {
+          kbeg = zz * kchunk;
+          kend = min(K, kbeg + kchunk);
+          nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
+          zero_acc();
+          kloop4(std::false_type{});
+          wait_dma_le<0>();
+#pragma unroll
+          for (int s = 0; s < SLOTS; ++s) sum[s] += piece(s);
+        }
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) set_piece(s, sum[s]);
+      }
+    } else if constexpr (SLOTS <= 16) {
       // ZB slices' loads in flight at a time
       constexpr int ZB = (128 / (SLOTS * 4)) < 1 ? 1 : ((128 / (SLOTS * 4)) > 8 ? 8 : (128 / (SLOTS * 4)));
       float4v sum[SLOTS];
@@ -725,7 +869,8 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
         const int grow = m0 + wm0 + 32 * ri + row;
         const int gcol = n0 + wn0 + 32 * rj + c4;
         if (grow < M && gcol < N) {  // N % 8 == 0: a 4-column chunk is all in or all out
-          const float rs = RESIDENT ? s_scale[grow - m0] : (rscale != nullptr ? rscale[grow] : 1.f);
+          const float rs = ((RESIDENT && !SPEC) || respec) ? s_scale[grow - m0]
+                                                          : (SPEC ? 1.f : (rscale != nullptr ? rscale[grow] : 1.f));
           const float4v b = bias != nullptr ? float4v{bias[gcol], bias[gcol + 1], bias[gcol + 2], bias[gcol + 3]}
                                             : float4v{0.f, 0.f, 0.f, 0.f};
           v = v * rs + b;
@@ -842,10 +987,26 @@ KSplit ksplit_for(int K, int ksplit) {
 
 template <bool OUT_F16>
 using GemmFn = void (*)(const _Float16*, const _Float16*, void*, const float*, const float*, float*, uint32_t*, int,
-                        int, int, int, int, int, int, const void*, int, int);
+                        int, int, int, int, int, int, const void*, int, int, _Float16*, int);
 
 template <bool OUT_F16>
-GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b, bool resident = false) {
+GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b, bool resident = false, bool spec = false) {
+  if (spec) {
+    // speculative fp16 A on the 4-wavefront tiles; the unsplit 32x128 tile with resident fallback
+    if (resident) return hgemm_kernel<Cfg32, OUT_F16, false, false, false, true, true>;
+    if (splitk) {
+      switch (t) {
+        case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, true, false, false, false, true>;
+        case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, true, false, false, false, true>;
+        default: return hgemm_kernel<Cfg32, OUT_F16, true, false, false, false, true>;
+      }
+    }
+    switch (t) {
+      case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, false, false, false, false, true>;
+      case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, false, false, false, false, true>;
+      default: return hgemm_kernel<Cfg32, OUT_F16, false, false, false, false, true>;
+    }
+  }
   if (resident) return hgemm_kernel<Cfg32, OUT_F16, false, false, false, true>;
   if (packed_b)
     return t == Tile::T256N ? hgemm_kernel<Cfg256n, OUT_F16, false, true, true> : hgemm_kernel<Cfg256, OUT_F16, false, true, true>;
@@ -896,10 +1057,28 @@ bool resident_route(const Plan& p, int ksplit, int K) {
   return p.tile == Tile::T32 && ksplit == 1 && K > 0 && ceil_div(K, Cfg32::BK) <= kResidentSteps;
 }
 
+// The fp16 activations of a speculative launch (mm_t's GEMM path in one launch for fp16 x on the
+// 4-wavefront tiles): the scratch for the rescaled cast of a recomputed tile (NULL on the
+// resident route, whose recomputation casts into LDS), log2 of the threshold, and the largest fp16
+// bit pattern not above it.
+struct SpecA {
+  _Float16* ys;
+  int texp;
+  int tbits;
+};
+
+// Largest fp16 bit pattern whose value is <= 2^texp (0x7bff, the largest finite, above it).
+int fp16_bits_at_most(int texp) {
+  if (texp >= 16) return 0x7bff;
+  if (texp >= -14) return (texp + 15) << 10;                // normal: exponent field texp + 15
+  if (texp >= -24) return 1 << (texp + 24);                 // subnormal: 2^texp = m * 2^-24
+  return 0;
+}
+
 int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, const float* bias, const float* rscale,
                 int M, int N, int K, int ksplit, int num_cus, void* ws, size_t ws_bytes, uint32_t* counters_in,
                 size_t counter_bytes_in, void* stream, bool packed = false, bool packed_b = false,
-                const ResidentCast* rc = nullptr) {
+                const ResidentCast* rc = nullptr, const SpecA* sp = nullptr) {
   if (M < 0 || N < 0 || K < 0 || K % 8 != 0 || N % 8 != 0 || K > kMaxK || N > kMaxN) return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
   if (ksplit < 1 || ksplit > 256) return G16_E_SPLIT;
@@ -909,6 +1088,10 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   if (num_cus <= 0) num_cus = stream_cus(static_cast<hipStream_t>(stream));
   Plan p = choose_tile(M, N, K, num_cus);
   if (rc != nullptr && !resident_route(p, ks.ksplit, K)) return G16_E_SHAPE;
+  const bool spec = sp != nullptr;
+  if (spec && ((p.tile != Tile::T128 && p.tile != Tile::T64 && p.tile != Tile::T32) || packed ||
+               (sp->ys == nullptr && !resident_route(p, ks.ksplit, K))))
+    return G16_E_SHAPE;
   if (packed) {
     // the packed layouts are the stage images of the 256-row tiles: the 256x256 tile, or the
     // 256x128 one where the plan picks it
@@ -929,14 +1112,18 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   const auto* b = reinterpret_cast<const _Float16*>(B);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool sk = ks.ksplit > 1;
-  const bool res = rc != nullptr;
-  const void* x = res ? rc->x : nullptr;
-  const int x_f32 = res ? rc->x_f32 : 0, texp = res ? rc->texp : 0;
+  // the speculative kernel on the resident route keeps its fallback in LDS (no ys)
+  const bool res = rc != nullptr || (spec && sp->ys == nullptr);
+  const void* x = rc != nullptr ? rc->x : (spec ? static_cast<const void*>(a) : nullptr);
+  const int x_f32 = rc != nullptr ? rc->x_f32 : 0;
+  const int texp = rc != nullptr ? rc->texp : (spec ? sp->texp : 0);
+  _Float16* ys = spec ? sp->ys : nullptr;
+  const int tbits = spec ? sp->tbits : 0;
   if (out_f16)
-    return launch(gemm_fn<true>(p.tile, sk, packed, packed_b, res), grid, block, s, a, b, C, bias, rscale, part, counters,
-                  M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp);
-  return launch(gemm_fn<false>(p.tile, sk, packed, packed_b, res), grid, block, s, a, b, C, bias, rscale, part, counters,
-                M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp);
+    return launch(gemm_fn<true>(p.tile, sk, packed, packed_b, res, spec), grid, block, s, a, b, C, bias, rscale, part,
+                  counters, M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp, ys, tbits);
+  return launch(gemm_fn<false>(p.tile, sk, packed, packed_b, res, spec), grid, block, s, a, b, C, bias, rscale, part,
+                counters, M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp, ys, tbits);
 }
 
 }  // namespace
@@ -1055,6 +1242,13 @@ bool mm_t_resident(int M, int N, int K, int num_cus) {
   return resident_route(choose_tile(M, N, K, num_cus), ksplit_for(K, g16_hgemm_plan(M, N, K, num_cus)).ksplit, K);
 }
 
+// fp16 x runs as one speculative launch wherever the plan is a 4-wavefront tile.
+bool mm_t_speculative(int M, int N, int K, int num_cus) {
+  if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0 || g16_hgemm_use_packed(M, N, K, num_cus) == 1) return false;
+  const Tile t = choose_tile(M, N, K, num_cus).tile;
+  return t == Tile::T128 || t == Tile::T64 || t == Tile::T32;
+}
+
 }  // namespace
 }  // namespace g16
 
@@ -1075,6 +1269,24 @@ extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, v
     return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
   if (out == nullptr || (K > 0 && (x == nullptr || w_t == nullptr))) return G16_E_NULL;
+  if (!x_is_f32 && g16::mm_t_speculative(M, N, K, num_cus)) {
+    // fp16 x on the 4-wavefront tiles: one launch that streams x as A (a row within the threshold
+    // is its own cast) and recomputes a tile from the rescaled cast only where some |x| exceeds it
+    const int texp = g16::thresh_exponent(thresh);
+    if (texp == -1000) return G16_E_SHAPE;
+    if (!g16::aligned16(x)) return G16_E_ALIGN;
+    const bool in_lds = g16::mm_t_resident(M, N, K, num_cus);
+    if (!in_lds) {
+      if (scratch == nullptr) return G16_E_NULL;
+      if (!g16::aligned16(scratch)) return G16_E_ALIGN;
+      if (scratch_bytes < g16_mm_t_scratch_bytes(M, N, K, num_cus)) return G16_E_WORKSPACE;
+    }
+    const g16::SpecA sp{in_lds ? nullptr : static_cast<_Float16*>(scratch), texp, g16::fp16_bits_at_most(texp)};
+    const int ks = g16_hgemm_plan(M, N, K, num_cus);
+    return g16::gemm_launch(static_cast<const uint16_t*>(x), w_t, out, out_is_f16 != 0, bias, nullptr, M, N, K, ks,
+                            num_cus, workspace, workspace_bytes, counters, counter_bytes, stream, false, false, nullptr,
+                            &sp);
+  }
   if (g16::mm_t_resident(M, N, K, num_cus)) {
     // one launch: the GEMM's workgroups cast their own rows into LDS (the same bits as the cast
     // below, the same GEMM arithmetic); no scratch

@@ -1,0 +1,190 @@
+"""One-launch small GEMMs for fp16 activations: on the 4-wavefront tiles (32x128, 64x128, 128x128,
+split or not), g16_mm_t_gemm streams x itself as A. A row whose |max| is within the threshold has
+scale 1, so its rowscale cast is x and the result is exactly the cast path's; where some |x| of a
+tile exceeds the threshold, that tile is computed again from the rescaled cast (in LDS on the
+resident route, else in the scratch buffer; by the last-arriving slice for split tiles).
+
+Every case is compared bit for bit with the reference's two-step sequence (rowscale cast, then
+GEMM: ops.py:86-108) run through the separate entry points g16_rowscale_f16 and g16_hgemm_* /
+g16_hgemm_splitk on the same planned route: tiles within the threshold (the streamed path) and
+tiles with rows above it (the recomputation), the threshold's edge, +inf and NaN entries, ragged
+M, N and K, fp16 and fp32 output with and without bias. Also: repeat calls bitwise equal and the
+split counters left zero, the public mm_t, the fp64 oracle, and HIP-graph replays.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from _inputs import outlier_rows, randn
+
+pytestmark = pytest.mark.gpu
+
+GEMM_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def lib(cuda):
+    from gtx16_fp16 import _clib
+
+    return _clib.load()
+
+
+@pytest.fixture(scope="module")
+def cus(cuda):
+    return torch.cuda.get_device_properties(cuda).multi_processor_count
+
+
+def _tile(lib, M, N, K, num_cus):
+    Kq = max(K, 128)
+    ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
+    area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
+    return area // 128
+
+
+def _bufs(lib, M, N, K, num_cus, dev):
+    ks = lib.g16_hgemm_plan(M, N, K, num_cus)
+    wsb = lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ks, num_cus) if ks > 1 else 0
+    cb = lib.g16_hgemm_splitk_counter_bytes(M, N, K, ks, num_cus) if ks > 1 else 0
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    cnt = torch.zeros(max(cb, 16), dtype=torch.uint8, device=dev)
+    return ks, ws, wsb, cnt, cb
+
+
+def _one_launch(lib, x, w, bias, out16, num_cus, bufs):
+    M, K = x.shape
+    N = w.shape[1]
+    ks, ws, wsb, cnt, cb = bufs
+    sb = lib.g16_mm_t_scratch_bytes(M, N, K, num_cus)
+    scratch = torch.empty(max(sb, 16), dtype=torch.uint8, device=x.device)
+    out = torch.empty(M, N, dtype=torch.float16 if out16 else torch.float32, device=x.device)
+    st = lib.g16_mm_t_gemm(x.data_ptr(), 0, w.data_ptr(), out.data_ptr(), 1 if out16 else 0,
+                           None if bias is None else bias.data_ptr(), 1024.0, M, N, K, num_cus,
+                           scratch.data_ptr() if sb else None, sb, ws.data_ptr() if wsb else None, wsb,
+                           cnt.data_ptr() if cb else None, cb, torch.cuda.current_stream(x.device).cuda_stream)
+    assert st == 0, lib.g16_strerror(st)
+    return out
+
+
+def _two_launches(lib, x, w, bias, out16, num_cus, bufs):
+    """The reference's sequence through the separate entry points: rowscale, then the GEMM on the
+    planned route (split-K where the plan splits)."""
+    M, K = x.shape
+    N = w.shape[1]
+    dev = x.device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ks, ws, wsb, cnt, cb = bufs
+    y = torch.empty(M, K, dtype=torch.float16, device=dev)
+    s = torch.empty(M, dtype=torch.float32, device=dev)
+    assert lib.g16_rowscale_f16(x.data_ptr(), y.data_ptr(), s.data_ptr(), M, K, 1024.0, stream) == 0
+    out = torch.empty(M, N, dtype=torch.float16 if out16 else torch.float32, device=dev)
+    b = None if bias is None else bias.data_ptr()
+    if ks > 1:
+        assert lib.g16_hgemm_splitk(y.data_ptr(), w.data_ptr(), out.data_ptr(), 1 if out16 else 0, b, s.data_ptr(),
+                                    M, N, K, ks, num_cus, ws.data_ptr(), wsb, cnt.data_ptr(), cb, stream) == 0
+    else:
+        gm = lib.g16_hgemm_f16out if out16 else lib.g16_hgemm_f32out
+        assert gm(y.data_ptr(), w.data_ptr(), out.data_ptr(), b, s.data_ptr(), M, N, K, stream) == 0
+    return out
+
+
+def _inputs(M, K, N, kind: str, seed: int, out16: bool):
+    """fp16 x: 'within' every |x| <= 1024 (the streamed path); 'over' some rows above it (the
+    recomputation); 'edge' one row at exactly 1024 and one a step above; 'special' +inf and NaN."""
+    x = randn((M, K), seed=seed)
+    if kind == "over":
+        x = outlier_rows(x, 0.1, 2e3, 8e3 if out16 else 6e4, seed=seed + 3)
+    elif kind == "edge":
+        x[0, K // 3] = 1024.0                         # at the threshold: scale 1
+        if M > 1:
+            x[M - 1, 0] = 1025.0                      # fp16 1025: above it, scale 2
+    elif kind == "special":
+        x[M // 2, K // 2] = float("inf")
+        if M > 2:
+            x[1, 0] = float("nan")
+    return x.to(torch.float16), randn((K, N), seed=seed + 1, scale=0.05, dtype=torch.float16)
+
+
+# (M, K, N, tile rows on 256 CUs, planned split on 256 CUs)
+ROUTES = [
+    (1024, 1024, 1024, 32, 1),    # C1: resident route (a recomputed tile casts into LDS)
+    (64, 1024, 1024, 32, 4),      # C3
+    (64, 4096, 1024, 32, 8),      # C3
+    (1024, 2048, 1024, 32, 1),    # unsplit 32x128 past the resident K: recomputes from the scratch
+    (100, 1000, 264, 32, 3),      # ragged M, N, K
+    (64, 4096, 11008, 64, 2),     # 64x128 split twice
+    (512, 4096, 4096, 128, 2),    # 128x128 split twice
+    (768, 4056, 4096, 128, 1),    # 128x128 unsplit, ragged K tail
+    (40, 8, 136, 32, 1),          # one K step of 8
+]
+KINDS = ["within", "over", "edge", "special"]
+
+
+@pytest.mark.parametrize("M,K,N,bm,ks", ROUTES)
+@pytest.mark.parametrize("kind", KINDS)
+def test_one_launch_equals_the_two_step_sequence_bitwise(lib, cus, cuda, M, K, N, bm, ks, kind):
+    if cus != 256:
+        pytest.skip(f"the route table is for 256 CUs (this device has {cus})")
+    assert _tile(lib, M, N, K, cus) == bm
+    assert lib.g16_hgemm_plan(M, N, K, cus) == ks
+    out16 = (M + K) % 2 == 0
+    use_bias = (N // 8) % 2 == 1
+    x, w = _inputs(M, K, N, kind, seed=M + K + N, out16=out16)
+    bias = randn((N,), seed=7, scale=0.1) if use_bias else None
+    xd, wd = x.to(cuda), w.to(cuda)
+    bd = None if bias is None else bias.to(cuda)
+    bits = (lambda t: t.view(torch.int16)) if out16 else (lambda t: t.view(torch.int32))
+    bufs = _bufs(lib, M, N, K, cus, cuda)
+    two = _two_launches(lib, xd, wd, bd, out16, cus, bufs)
+    one = _one_launch(lib, xd, wd, bd, out16, cus, bufs)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(one), bits(two))
+    again = [_one_launch(lib, xd, wd, bd, out16, cus, bufs) for _ in range(5)]
+    torch.cuda.synchronize()
+    for o in again:
+        assert torch.equal(bits(o), bits(one))
+    assert int(bufs[3].count_nonzero()) == 0  # split counters (and their flag) left zero
+    import gtx16_fp16 as g
+
+    pub = g.mm_t(xd, wd, bd, torch.float16 if out16 else torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(pub), bits(one))
+    if kind in ("within", "over", "edge"):
+        ref = oracle.mm_t(x.numpy(), w.numpy(), None if bias is None else bias.numpy(),
+                          "float16" if out16 else "float32")
+        assert oracle.rel_err(one.cpu().numpy(), ref) <= GEMM_TOL
+
+
+def test_graph_replays_of_speculative_mm_t_match_eager(cuda):
+    import gtx16_fp16 as g
+
+    shapes = [(1024, 1024, 1024, "within"), (64, 4096, 1024, "over"), (100, 1000, 264, "over"),
+              (512, 4096, 4096, "within")]
+    xs, ws = [], []
+    for i, (M, K, N, kind) in enumerate(shapes):
+        x, w = _inputs(M, K, N, kind, seed=40 + i, out16=False)
+        xs.append(x.to(cuda))
+        ws.append(w.to(cuda))
+    eager = [g.mm_t(x, w, None, torch.float32) for x, w in zip(xs, ws)]
+    s = torch.cuda.Stream(cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for x, w in zip(xs, ws):
+            g.mm_t(x, w, None, torch.float32)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            outs = [g.mm_t(x, w, None, torch.float32) for x, w in zip(xs, ws)]
+    torch.cuda.current_stream(cuda).wait_stream(s)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for o in outs:
+            o.fill_(0.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e)
+        extra = g.mm_t(xs[1], ws[1], None, torch.float32)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(extra, eager[1])
