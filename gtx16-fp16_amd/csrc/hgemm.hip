@@ -53,6 +53,8 @@
 //     device-coherent stores); the last slice to arrive adds all slices in slice order and runs the
 //     epilogue. Deterministic, and bias/scale/cast are fused (the reference prefills C with the bias
 //     and adds with fp32 atomics, kernels.py:119-122, ops.py:54-62).
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "g16_common.hpp"
@@ -66,9 +68,6 @@ constexpr int kSplitAlign = 64;  // split-K slices start on a multiple of every 
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every descriptor's range: reads 0
 
 typedef short short4v __attribute__((ext_vector_type(4)));
-typedef unsigned short u16x2v __attribute__((ext_vector_type(2)));
-typedef unsigned short u16x4v __attribute__((ext_vector_type(4)));
-typedef unsigned short u16x8v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) short4v lds_short4v;
 
@@ -205,8 +204,11 @@ __device__ inline uint32_t arrive_add_coherent(uint32_t* counter, uint32_t add) 
   __syncthreads();
   return s_val;
 }
-// A speculative slice whose A exceeded the threshold adds this on top of its arrival.
-constexpr uint32_t kSpecFlag = 1u << 16;
+// Split counter of a speculative launch: the arrival count in the low kSpecShift bits, and bit
+// kSpecShift + z set by slice z if its A exceeded the threshold (each slice adds its own bit once,
+// so the fields never carry into each other).
+constexpr int kSpecShift = 8;
+constexpr int kSpecMaxSplit = 32 - kSpecShift;
 
 // Workgroup barrier without the counter waits __syncthreads() adds: the caller has already waited
 // for exactly the memory operations the next phase depends on. The memory clobber keeps the
@@ -215,9 +217,12 @@ __device__ inline void phase_barrier() { asm volatile("s_barrier" ::: "memory");
 
 // RESIDENT: A is unused; the kernel casts X (fp32 when x_f32, else fp16; threshold 2^texp) itself
 // into resident LDS stages (the 32x128 tile, unsplit, K <= kResidentSteps * BK).
-// SPEC: A (and X) are the fp16 activations, streamed as they are; tbits is the largest fp16 bit
-// pattern not above the threshold. A tile with a larger |x| is recomputed from the rescaled cast:
-// in the resident LDS stages (with RESIDENT) or in ys (row-major, M x K fp16).
+// SPEC: A is the fp16 activations, streamed as they are; tbits is the largest fp16 bit pattern
+// not above the threshold 2^texp (texp >= -8, so every row exponent is <= 24). A tile with a larger
+// |x| (or a NaN) is computed again with its A fragments rescaled in registers: unsplit, by the same
+// workgroup; split, by the slice that arrives last, over every slice in slice order. A split
+// slice that saw such a value publishes its rows' |max| in place of its partial tile. A tile that
+// is computed again stores 1 into *spec_miss (when not NULL; pinned host memory).
 template <class Cfg, bool OUT_F16, bool SPLITK, bool PACKED_A = false, bool PACKED_B = false, bool RESIDENT = false,
           bool SPEC = false>
 __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
@@ -226,16 +231,18 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
                                                          uint32_t* __restrict__ counters, int M, int N, int K,
                                                          int kchunk, int ksplit, int ntm, int ntn,
                                                          const void* __restrict__ X, int x_f32, int texp,
-                                                         _Float16* __restrict__ ys, int tbits) {
+                                                         int tbits, uint32_t* __restrict__ spec_miss) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN, MB = Cfg::MB, MK = Cfg::MK;
   constexpr int BK = Cfg::BK, NSTAGE = Cfg::NSTAGE;
   static_assert(!RESIDENT || (Cfg::BM == 32 && Cfg::BK == 64 && Cfg::WAVES == 4 && !SPLITK && !PACKED_A && !PACKED_B),
                 "resident A: the unsplit 32x128 tile");
-  static_assert(!SPEC || (Cfg::WAVES == 4 && !Cfg::MF16 && !PACKED_A && !PACKED_B), "speculative A: the 4-wavefront tiles");
+  static_assert(!SPEC || (Cfg::WAVES == 4 && !Cfg::MF16 && !PACKED_A && !PACKED_B && !RESIDENT),
+                "speculative A: the 4-wavefront tiles, 32x32x16 blocks (lane l's A rows are l % 32)");
   constexpr int A_STAGES = RESIDENT ? kResidentSteps : NSTAGE;
   __shared__ __attribute__((aligned(1024))) unsigned char sA[A_STAGES][Cfg::A_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char sB[NSTAGE][Cfg::B_BYTES];
   __shared__ float s_scale[(RESIDENT || SPEC) ? BM : 1];
+  __shared__ float s_rowmax[SPEC ? BM : 1];  // speculative recomputation: the rows' |max|, then 2^-e
   const uint32_t sA_lds = lds_base(&sA[0][0]), sB_lds = lds_base(&sB[0][0]);
 
   // ---- tile assignment (XCD-aware, grouped) ----
@@ -275,7 +282,6 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // DMA of K step k0 into stage `st`, one 1 KB instruction at a time (instruction d < A_INSTR: A,
   // else B). Steps past the slice are all out of range (zeros, no traffic): they keep the number
   // of DMA operations per step constant, which the vmcnt waits rely on.
-  const _Float16* a_src = A;  // row-major A: the activations, or the speculative path's rescaled cast
   auto rsrc_a = [&](int k0) {
     if constexpr (PACKED_A) {
       static_assert(Cfg::BM == 256 && Cfg::BK == 32 && !SPLITK, "packed A is the stage image of 256 rows x 32 K");
@@ -283,7 +289,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
           const_cast<_Float16*>(A) + static_cast<size_t>(tm) * ceil_div(K, BK) * (Cfg::A_BYTES / 2), 0, 0x7fffffff,
           kRawBufferDword3);
     } else {
-      return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a_src) + static_cast<size_t>(m0) * K + k0, 0,
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A) + static_cast<size_t>(m0) * K + k0, 0,
                                                0x7fffffff, kRawBufferDword3);
     }
   };
@@ -392,24 +398,39 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // of step j run on set j&1 while the LDS reads of step j+1 fill set (j+1)&1.
   constexpr int KS = BK / MK;
   half8 af[2][KS][TM], bf[2][KS][TN];
-  // Speculative A: the largest |x| this lane has multiplied, per fp16 half of a dword, as the bit
-  // pattern shifted left by one (the shift drops the sign; fp16 magnitudes order like their bits;
-  // a NaN counts as large, which only costs a recompute).
-  u16x2v amax_pk = {0, 0};
+  // Speculative A: the largest and smallest x this lane has multiplied, per fragment row i and per
+  // fp16 half of a dword (lane l's A fragments i are all of row wm0 + 32 i + l % 32). The IEEE
+  // maximum/minimum propagate a NaN, so a NaN counts as above the threshold, which only costs a
+  // recompute. Chains of two become v_pk_maximum3_f16 / v_pk_minimum3_f16: 4 VALU instructions per
+  // 8-value fragment.
+  half2v xmax[TM] = {}, xmin[TM] = {};
   auto track_amax = [&](int buf) {
     if constexpr (SPEC) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-          // Whole-vector shuffles only: hipcc lowers __builtin_bit_cast of one element of a
-          // vector (u.y) as a read of element 0, so such a form would see 2 of every 8 halves.
-          const u16x8v u = __builtin_bit_cast(u16x8v, af[buf][ks][i]) << static_cast<unsigned short>(1);
-          const u16x4v q = __builtin_elementwise_max(__builtin_shufflevector(u, u, 0, 1, 2, 3),
-                                                     __builtin_shufflevector(u, u, 4, 5, 6, 7));
-          amax_pk = __builtin_elementwise_max(
-              amax_pk, __builtin_elementwise_max(__builtin_shufflevector(q, q, 0, 1), __builtin_shufflevector(q, q, 2, 3)));
+          const half8 v = af[buf][ks][i];
+          const half2v d0 = __builtin_shufflevector(v, v, 0, 1), d1 = __builtin_shufflevector(v, v, 2, 3);
+          const half2v d2 = __builtin_shufflevector(v, v, 4, 5), d3 = __builtin_shufflevector(v, v, 6, 7);
+          xmax[i] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(xmax[i], d0), d1);
+          xmax[i] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(xmax[i], d2), d3);
+          xmin[i] = __builtin_elementwise_minimum(__builtin_elementwise_minimum(xmin[i], d0), d1);
+          xmin[i] = __builtin_elementwise_minimum(__builtin_elementwise_minimum(xmin[i], d2), d3);
         }
+    }
+  };
+  // The recomputation's cast: fp16_rne(x * 2^-e) of each fragment row, as one fp16 multiply by the
+  // row's factor 2^-e (0 for a row whose scale is +inf): the product is exact before rounding, and
+  // fp16 denormals are kept, so it is the rowscale cast's value bit for bit (e <= 24 here).
+  half2v fac[TM];
+  auto scale_frags = [&](int buf) {
+    if constexpr (SPEC) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[buf][ks][i] *= __builtin_shufflevector(fac[i], fac[i], 0, 1, 0, 1, 0, 1, 0, 1);
     }
   };
   // fragment read f of a step: f = ks * (TM + TN) + (i < TM ? i : TM + j)
@@ -535,9 +556,11 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // see a steady trickle between barriers.
   constexpr int LAG = NSTAGE - 2;
   // One pass of the K loop over [kbeg, kend) into acc, with A streamed through the ring (RES
-  // false) or cast into the resident stages first (RES true).
-  auto kloop4 = [&](auto resc) {
+  // false) or cast into the resident stages first (RES true); RESCALE: the speculative path's
+  // recomputation, which scales the streamed A fragments by their rows' factors before use.
+  auto kloop4 = [&](auto resc, auto rescale) {
     constexpr bool RES = decltype(resc)::value;
+    constexpr bool RESCALE = decltype(rescale)::value;
     // DMA instructions per step: A and B, or B alone with resident A
     constexpr int DMA0 = RES ? Cfg::A_INSTR : 0;
     constexpr int PARTS = NDMA - DMA0;
@@ -577,7 +600,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       // resident A: step j+1's own stage (the last step reads an in-range stage it does not use)
       const int sta = RES ? (j + 1 < nk ? j + 1 : j) : -1;
       const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
-      if constexpr (SPEC && !RES) track_amax(H);  // step j's A fragments (streamed x)
+      if constexpr (RESCALE) scale_frags(H);
 #pragma unroll
       for (int p = 0; p < PARTS; ++p) {
         dma_op(std_, kd, ra, rb, DMA0 + p);
@@ -588,6 +611,8 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
         for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f, sta);
         __builtin_amdgcn_sched_barrier(0);
       }
+      // step j's A fragments (streamed x), after the step's MFMAs have been issued on them
+      if constexpr (SPEC && !RES && !RESCALE) track_amax(H);
       wait_dma_le<LAG * PARTS>();  // step j+2 has landed (this wavefront's part)
       __syncthreads();            // ... every wavefront's part; step j+1 is in registers
     };
@@ -651,8 +676,8 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     }
     if (grp == 0) phase_barrier();  // every wavefront passes the same number of barriers
   } else {
-    if constexpr (RESIDENT && !SPEC) kloop4(std::true_type{});
-    else kloop4(std::false_type{});
+    if constexpr (RESIDENT) kloop4(std::true_type{}, std::false_type{});
+    else kloop4(std::false_type{}, std::false_type{});
   }
   wait_dma_le<0>();  // no DMA may still be writing LDS past this point
   if (stamps && tid == 0) {
@@ -660,53 +685,85 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     g_loop_clock[1] = __builtin_amdgcn_s_memrealtime() - clk_r0;
   }
 
-  // ---- speculative A: recompute from the rescaled cast where some |x| exceeded the threshold ----
-  bool respec = false;  // acc comes from the rescaled cast, with the row scales in s_scale
+  // ---- speculative A: recompute the tile where some |x| exceeded the threshold ----
+  bool respec = false;  // acc comes from the rescaled A, with the row scales in s_scale
   auto zero_acc = [&]() {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
   };
-  // This tile's rows of x over all of K, cast as the rowscale kernel casts them (same arithmetic)
-  // into ys, their scales into s_scale; one wavefront per row. Other workgroups of the tile row
-  // may write the same rows at the same time, with the same bits.
-  auto cast_rows_to_ys = [&]() {
+  // max with a NaN in either operand giving NaN
+  auto nan_max = [](float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); };
+  // this lane's rows' |max| over the K range it has multiplied (lanes l and l ^ 32 hold the same
+  // row, different k), NaN where a NaN was seen
+  float ramax[TM];
+  int over = 0;  // some row of this slice exceeded the threshold or held a NaN (the workgroup agrees)
+  if constexpr (SPEC) {
+    // the largest fp16 value not above the threshold; a NaN fails the comparison
+    const float t = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(tbits)));
+    bool within = true;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float a = nan_max(nan_max(static_cast<float>(xmax[i].x), static_cast<float>(xmax[i].y)),
+                        nan_max(-static_cast<float>(xmin[i].x), -static_cast<float>(xmin[i].y)));
+      a = nan_max(a, __shfl_xor(a, 32));
+      ramax[i] = a;
+      within = within && a <= t;
+    }
+    over = __syncthreads_or(within ? 0 : 1);
+  }
+  // With s_rowmax holding every row's |max| (NaN where a NaN was seen): the rows' exponents, exactly
+  // as the rowscale cast derives them, into s_scale (2^e) and this lane's factors fac (2^-e). A
+  // row with a NaN gets its |max| over all of K from x itself, NaN dropped as the cast drops it.
+  auto row_factors = [&]() {
     if constexpr (SPEC) {
-      const int rows = min(BM, M - m0);
-      const int nch = K / 8;
-      for (int r = wave; r < rows; r += Cfg::WAVES) {
-        const u32x4* xr = reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m0 + r) * K);
-        float am = 0.f;
-        for (int idx = lane; idx < nch; idx += kWave) am = chunk_absmax(am, xr[idx], _Float16{});
-        am = wave_max(am);
+      for (int r = wave; r < BM; r += Cfg::WAVES) {
+        const float v = s_rowmax[r];
+        if (v != v) {
+          float am = 0.f;
+          if (m0 + r < M) {
+            const u32x4* xr = reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m0 + r) * K);
+            for (int idx = lane; idx < K / 8; idx += kWave) am = chunk_absmax(am, xr[idx], _Float16{});
+          }
+          am = wave_max(am);
+          if (lane == 0) s_rowmax[r] = am;
+        }
+      }
+      __syncthreads();
+      if (tid < BM) {
         int e;
         float sc;
-        row_exponent(am, texp, e, sc);
-        if (lane == 0) s_scale[r] = sc;
-        u32x4* yr = reinterpret_cast<u32x4*>(ys + static_cast<size_t>(m0 + r) * K);
-        for (int idx = lane; idx < nch; idx += kWave) yr[idx] = cast_scaled(xr[idx], e, _Float16{});
+        row_exponent(s_rowmax[tid], texp, e, sc);
+        s_scale[tid] = sc;
+        s_rowmax[tid] = e == kInfExp ? 0.f : ldexpf(1.f, -e);
       }
-      __builtin_amdgcn_s_waitcnt(0);  // the cast is in L2 before this workgroup's DMA reads it
       __syncthreads();
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const _Float16 f = static_cast<_Float16>(s_rowmax[wm0 + 32 * i + (lane & 31)]);
+        fac[i] = half2v{f, f};
+      }
     }
   };
-  int over = 0;  // some |x| of this slice exceeded the threshold (the whole workgroup agrees)
-  if constexpr (SPEC) {
-    const uint32_t lane_max = amax_pk.x > amax_pk.y ? amax_pk.x : amax_pk.y;
-    over = __syncthreads_or(lane_max > (static_cast<uint32_t>(tbits) << 1) ? 1 : 0);
-  }
+  // the wavefronts of the first column hold every row once: lanes < 32 write them
+  const bool row_writer = wave % Cfg::WGN == 0 && lane < 32;
+  // a recomputation is remembered for the weight (the host routes its next calls around it)
+  auto note_miss = [&]() {
+    if (spec_miss != nullptr && tid == 0) __hip_atomic_store(spec_miss, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  };
   if constexpr (SPEC && !SPLITK) {
     if (over) {
       respec = true;
-      zero_acc();
-      if constexpr (RESIDENT) {
-        kloop4(std::true_type{});  // cast into the resident stages (and s_scale), then the K loop
-      } else {
-        cast_rows_to_ys();
-        a_src = ys;
-        kloop4(std::false_type{});
+      note_miss();
+      if (row_writer) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) s_rowmax[wm0 + 32 * i + lane] = ramax[i];
       }
+      __syncthreads();
+      row_factors();
+      zero_acc();
+      kloop4(std::false_type{}, std::true_type{});
       wait_dma_le<0>();
     }
   }
@@ -744,24 +801,47 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     auto slot_off = [&](int z, int s) {
       return static_cast<uint32_t>(z) * TILE_BYTES + static_cast<uint32_t>((wave * SLOTS + s) * 64 + lane) * 16u;
     };
+    // the speculative path's rows' |max| of slice z: the first BM floats of its partial tile
+    auto rowmax_slot = [&](int zz) { return part + (static_cast<size_t>(tile) * ksplit + zz) * (BM * BN); };
+    if (SPEC && over) {
+      // the last slice recomputes this tile: publish the rows' |max| in place of the partial tile
+      if (row_writer) {
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) store_coherent4(slices, slot_off(z, s), piece(s));
+        for (int i = 0; i < TM; ++i) store_coherent(rowmax_slot(z) + wm0 + 32 * i + lane, ramax[i]);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < SLOTS; ++s) store_coherent4(slices, slot_off(z, s), piece(s));
+    }
     if constexpr (SPEC) {
-      const uint32_t total = arrive_add_coherent(counters + tile * kCounterStride, over ? 1u + kSpecFlag : 1u);
-      if ((total & (kSpecFlag - 1u)) != static_cast<uint32_t>(ksplit)) return;
-      respec = total >= kSpecFlag;
+      const uint32_t total = arrive_add_coherent(counters + tile * kCounterStride,
+                                                 1u + (over ? (1u << (kSpecShift + z)) : 0u));
+      if ((total & ((1u << kSpecShift) - 1u)) != static_cast<uint32_t>(ksplit)) return;
+      respec = (total >> kSpecShift) != 0u;
+      if (respec) {
+        // a row's |max| over K: the largest over the slices that saw a value above the threshold
+        // (the others hold none, so they cannot raise a row's exponent above 0)
+        const uint32_t mask = total >> kSpecShift;
+        if (tid < BM) {
+          float m = 0.f;
+          for (int zz = 0; zz < ksplit; ++zz)
+            if ((mask >> zz) & 1u) m = nan_max(m, load_coherent(rowmax_slot(zz) + tid));
+          s_rowmax[tid] = m;
+        }
+        __syncthreads();
+      }
     } else {
       if (!arrive_last_coherent(counters + tile * kCounterStride, static_cast<uint32_t>(ksplit))) return;
     }
     // Slices are added in slice order (every slice, this one's included, is read back from the
     // workspace), so each output is the same sum whichever slice arrives last.
     if (SPEC && respec) {
-      // Some slice's A exceeded the threshold: recompute every slice from the rescaled cast and add
+      // Some slice's A exceeded the threshold: recompute every slice with the rescaled A and add
       // them in slice order, exactly as the reduction below adds the published slices.
       if constexpr (SPEC) {
         static_assert(SLOTS <= 16, "the 4-wavefront tiles");
-        cast_rows_to_ys();
-        a_src = ys;
+        note_miss();
+        row_factors();
         float4v sum[SLOTS];
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -770,7 +850,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
           kend = min(K, kbeg + kchunk);
           nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
           zero_acc();
-          kloop4(std::false_type{});
+          kloop4(std::false_type{}, std::true_type{});
           wait_dma_le<0>();
 #pragma unroll
           for (int s = 0; s < SLOTS; ++s) sum[s] += piece(s);
@@ -869,8 +949,8 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
         const int grow = m0 + wm0 + 32 * ri + row;
         const int gcol = n0 + wn0 + 32 * rj + c4;
         if (grow < M && gcol < N) {  // N % 8 == 0: a 4-column chunk is all in or all out
-          const float rs = ((RESIDENT && !SPEC) || respec) ? s_scale[grow - m0]
-                                                          : (SPEC ? 1.f : (rscale != nullptr ? rscale[grow] : 1.f));
+          const float rs = (RESIDENT || respec) ? s_scale[grow - m0]
+                                                : (SPEC ? 1.f : (rscale != nullptr ? rscale[grow] : 1.f));
           const float4v b = bias != nullptr ? float4v{bias[gcol], bias[gcol + 1], bias[gcol + 2], bias[gcol + 3]}
                                             : float4v{0.f, 0.f, 0.f, 0.f};
           v = v * rs + b;
@@ -987,13 +1067,12 @@ KSplit ksplit_for(int K, int ksplit) {
 
 template <bool OUT_F16>
 using GemmFn = void (*)(const _Float16*, const _Float16*, void*, const float*, const float*, float*, uint32_t*, int,
-                        int, int, int, int, int, int, const void*, int, int, _Float16*, int);
+                        int, int, int, int, int, int, const void*, int, int, int, uint32_t*);
 
 template <bool OUT_F16>
 GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b, bool resident = false, bool spec = false) {
   if (spec) {
-    // speculative fp16 A on the 4-wavefront tiles; the unsplit 32x128 tile with resident fallback
-    if (resident) return hgemm_kernel<Cfg32, OUT_F16, false, false, false, true, true>;
+    // speculative fp16 A on the 4-wavefront tiles
     if (splitk) {
       switch (t) {
         case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, true, false, false, false, true>;
@@ -1057,15 +1136,17 @@ bool resident_route(const Plan& p, int ksplit, int K) {
   return p.tile == Tile::T32 && ksplit == 1 && K > 0 && ceil_div(K, Cfg32::BK) <= kResidentSteps;
 }
 
-// The fp16 activations of a speculative launch (mm_t's GEMM path in one launch for fp16 x on the
-// 4-wavefront tiles): the scratch for the rescaled cast of a recomputed tile (NULL on the
-// resident route, whose recomputation casts into LDS), log2 of the threshold, and the largest fp16
-// bit pattern not above it.
+// A speculative launch (mm_t's GEMM path in one launch for fp16 x on the 4-wavefront tiles): log2
+// of the threshold (>= kSpecMinTexp), the largest fp16 bit pattern not above it, and the weight's
+// history slot (or NULL).
 struct SpecA {
-  _Float16* ys;
   int texp;
   int tbits;
+  uint32_t* miss;
 };
+// Row exponents stay <= 16 - texp (fp16 |x| < 2^16): with texp >= -8, every factor 2^-e of the
+// recomputation is an fp16 value.
+constexpr int kSpecMinTexp = -8;
 
 // Largest fp16 bit pattern whose value is <= 2^texp (0x7bff, the largest finite, above it).
 int fp16_bits_at_most(int texp) {
@@ -1090,7 +1171,7 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   if (rc != nullptr && !resident_route(p, ks.ksplit, K)) return G16_E_SHAPE;
   const bool spec = sp != nullptr;
   if (spec && ((p.tile != Tile::T128 && p.tile != Tile::T64 && p.tile != Tile::T32) || packed ||
-               (sp->ys == nullptr && !resident_route(p, ks.ksplit, K))))
+               ks.ksplit > kSpecMaxSplit || sp->texp < kSpecMinTexp))
     return G16_E_SHAPE;
   if (packed) {
     // the packed layouts are the stage images of the 256-row tiles: the 256x256 tile, or the
@@ -1112,18 +1193,17 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   const auto* b = reinterpret_cast<const _Float16*>(B);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool sk = ks.ksplit > 1;
-  // the speculative kernel on the resident route keeps its fallback in LDS (no ys)
-  const bool res = rc != nullptr || (spec && sp->ys == nullptr);
-  const void* x = rc != nullptr ? rc->x : (spec ? static_cast<const void*>(a) : nullptr);
-  const int x_f32 = rc != nullptr ? rc->x_f32 : 0;
-  const int texp = rc != nullptr ? rc->texp : (spec ? sp->texp : 0);
-  _Float16* ys = spec ? sp->ys : nullptr;
+  const bool res = rc != nullptr;
+  const void* x = res ? rc->x : nullptr;
+  const int x_f32 = res ? rc->x_f32 : 0;
+  const int texp = res ? rc->texp : (spec ? sp->texp : 0);
   const int tbits = spec ? sp->tbits : 0;
+  uint32_t* miss = spec ? sp->miss : nullptr;
   if (out_f16)
     return launch(gemm_fn<true>(p.tile, sk, packed, packed_b, res, spec), grid, block, s, a, b, C, bias, rscale, part,
-                  counters, M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp, ys, tbits);
+                  counters, M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp, tbits, miss);
   return launch(gemm_fn<false>(p.tile, sk, packed, packed_b, res, spec), grid, block, s, a, b, C, bias, rscale, part,
-                counters, M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp, ys, tbits);
+                counters, M, N, K, ks.kchunk, ks.ksplit, p.ntm, p.ntn, x, x_f32, texp, tbits, miss);
 }
 
 }  // namespace
@@ -1242,6 +1322,55 @@ bool mm_t_resident(int M, int N, int K, int num_cus) {
   return resident_route(choose_tile(M, N, K, num_cus), ksplit_for(K, g16_hgemm_plan(M, N, K, num_cus)).ksplit, K);
 }
 
+// Speculation history, per device: a speculative launch that had to compute a tile again stores 1
+// into its weight's slot (pinned host memory, written by the kernel). g16_mm_t_gemm then sends the
+// weight's next kSpecRetry - 1 calls down the resident or two-launch route (the same result bits,
+// without the recomputation) and speculates again after that. Weights whose pointers hash alike
+// share a slot; the route never changes a result, only its time.
+constexpr int kSpecSlots = 1024;
+constexpr uint32_t kSpecRetry = 64;
+struct SpecHistory {
+  uint32_t* miss = nullptr;                  // kSpecSlots words (hipHostMalloc, never freed)
+  std::atomic<uint32_t> routed[kSpecSlots];  // calls routed around speculation since the slot's miss
+};
+
+size_t spec_slot(const void* w_t) {
+  const uint64_t h = (static_cast<uint64_t>(reinterpret_cast<uintptr_t>(w_t)) >> 8) * 0x9e3779b97f4a7c15ull;
+  return static_cast<size_t>(h >> 54);  // top 10 bits: kSpecSlots
+}
+static_assert(kSpecSlots == 1024, "spec_slot keeps 10 bits");
+
+// The history of the device that owns `stream`, allocated on first use; NULL while that stream is
+// being captured into a graph before then (no allocation during a capture) or if allocation fails.
+SpecHistory* spec_history(hipStream_t stream) {
+  static std::atomic<SpecHistory*> hist[64];
+  static std::mutex mu;
+  int dev = 0;
+  if (stream == nullptr || hipStreamGetDevice(stream, &dev) != hipSuccess) {
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  }
+  if (dev < 0 || dev >= 64) return nullptr;
+  SpecHistory* h = hist[dev].load(std::memory_order_acquire);
+  if (h != nullptr) return h;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (stream != nullptr && (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone))
+    return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  h = hist[dev].load(std::memory_order_acquire);
+  if (h != nullptr) return h;
+  void* p = nullptr;
+  if (hipHostMalloc(&p, kSpecSlots * sizeof(uint32_t), hipHostMallocPortable | hipHostMallocCoherent) != hipSuccess) {
+    (void)hipGetLastError();  // leave no error behind for the caller's next check
+    return nullptr;
+  }
+  __builtin_memset(p, 0, kSpecSlots * sizeof(uint32_t));
+  h = new SpecHistory;
+  h->miss = static_cast<uint32_t*>(p);
+  for (auto& r : h->routed) r.store(0, std::memory_order_relaxed);
+  hist[dev].store(h, std::memory_order_release);
+  return h;
+}
+
 // fp16 x runs as one speculative launch wherever the plan is a 4-wavefront tile.
 bool mm_t_speculative(int M, int N, int K, int num_cus) {
   if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0 || g16_hgemm_use_packed(M, N, K, num_cus) == 1) return false;
@@ -1269,29 +1398,43 @@ extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, v
     return G16_E_SHAPE;
   if (M == 0 || N == 0) return G16_OK;
   if (out == nullptr || (K > 0 && (x == nullptr || w_t == nullptr))) return G16_E_NULL;
-  if (!x_is_f32 && g16::mm_t_speculative(M, N, K, num_cus)) {
+  const int texp = g16::thresh_exponent(thresh);
+  if (texp == -1000) return G16_E_SHAPE;
+  if (!x_is_f32 && texp >= g16::kSpecMinTexp && g16::mm_t_speculative(M, N, K, num_cus)) {
     // fp16 x on the 4-wavefront tiles: one launch that streams x as A (a row within the threshold
-    // is its own cast) and recomputes a tile from the rescaled cast only where some |x| exceeds it
-    const int texp = g16::thresh_exponent(thresh);
-    if (texp == -1000) return G16_E_SHAPE;
-    if (!g16::aligned16(x)) return G16_E_ALIGN;
-    const bool in_lds = g16::mm_t_resident(M, N, K, num_cus);
-    if (!in_lds) {
-      if (scratch == nullptr) return G16_E_NULL;
-      if (!g16::aligned16(scratch)) return G16_E_ALIGN;
-      if (scratch_bytes < g16_mm_t_scratch_bytes(M, N, K, num_cus)) return G16_E_WORKSPACE;
+    // is its own cast) and computes a tile again, with A rescaled in registers, only where some
+    // |x| exceeds it; no scratch. Where the caller's scratch allows the other route, a weight
+    // whose recent call was computed again takes that route for a while instead.
+    const bool other_route =
+        g16::mm_t_resident(M, N, K, num_cus) ||
+        (scratch != nullptr && g16::aligned16(scratch) && scratch_bytes >= g16_mm_t_scratch_bytes(M, N, K, num_cus));
+    bool speculate = true;
+    uint32_t* miss = nullptr;
+    if (other_route) {
+      if (g16::SpecHistory* h = g16::spec_history(static_cast<hipStream_t>(stream))) {
+        const size_t slot = g16::spec_slot(w_t);
+        miss = h->miss + slot;
+        if (__atomic_load_n(miss, __ATOMIC_RELAXED) != 0u) {
+          if (h->routed[slot].fetch_add(1, std::memory_order_relaxed) + 1 < g16::kSpecRetry) {
+            speculate = false;
+          } else {
+            h->routed[slot].store(0, std::memory_order_relaxed);
+            __atomic_store_n(miss, 0u, __ATOMIC_RELAXED);
+          }
+        }
+      }
     }
-    const g16::SpecA sp{in_lds ? nullptr : static_cast<_Float16*>(scratch), texp, g16::fp16_bits_at_most(texp)};
-    const int ks = g16_hgemm_plan(M, N, K, num_cus);
-    return g16::gemm_launch(static_cast<const uint16_t*>(x), w_t, out, out_is_f16 != 0, bias, nullptr, M, N, K, ks,
-                            num_cus, workspace, workspace_bytes, counters, counter_bytes, stream, false, false, nullptr,
-                            &sp);
+    if (speculate) {
+      const g16::SpecA sp{texp, g16::fp16_bits_at_most(texp), miss};
+      const int ks = g16_hgemm_plan(M, N, K, num_cus);
+      return g16::gemm_launch(static_cast<const uint16_t*>(x), w_t, out, out_is_f16 != 0, bias, nullptr, M, N, K, ks,
+                              num_cus, workspace, workspace_bytes, counters, counter_bytes, stream, false, false,
+                              nullptr, &sp);
+    }
   }
   if (g16::mm_t_resident(M, N, K, num_cus)) {
     // one launch: the GEMM's workgroups cast their own rows into LDS (the same bits as the cast
     // below, the same GEMM arithmetic); no scratch
-    const int texp = g16::thresh_exponent(thresh);
-    if (texp == -1000) return G16_E_SHAPE;
     if (!g16::aligned16(x)) return G16_E_ALIGN;
     const g16::ResidentCast rc{x, x_is_f32 != 0 ? 1 : 0, texp};
     return g16::gemm_launch(nullptr, w_t, out, out_is_f16 != 0, bias, nullptr, M, N, K, 1, num_cus, nullptr, 0, nullptr,
@@ -1317,6 +1460,11 @@ extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, v
   const int ks = g16_hgemm_plan(M, N, K, num_cus);
   return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, ks, num_cus, workspace, workspace_bytes,
                           counters, counter_bytes, stream);
+}
+
+extern "C" int g16_mm_t_spec_paused(const uint16_t* w_t, void* stream) {
+  const g16::SpecHistory* h = g16::spec_history(static_cast<hipStream_t>(stream));
+  return h != nullptr && __atomic_load_n(h->miss + g16::spec_slot(w_t), __ATOMIC_RELAXED) != 0u ? 1 : 0;
 }
 
 extern "C" int g16_gemm_clock(unsigned long long* dst, void* stream) {

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 12
+#define G16_ABI_VERSION 13
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -126,12 +126,20 @@ int g16_hgemm_use_packed(int M, int N, int K, int num_cus);
  * ksplit = g16_hgemm_plan() when that is > 1, else the plain GEMM. The same result bits as the
  * separate entry points (rowscale, then GEMM); one call instead of two on a path whose small
  * shapes are bound by host and launch time. No counterpart kernel in the reference.
- *   One launch: where the plan is the unsplit 32x128 tile and K <= 1280, the GEMM's workgroups
- *   cast their own rows of x into LDS (the rowscale arithmetic, the same bits) and no rowscale
- *   launch runs; g16_mm_t_scratch_bytes() is then 0 and scratch may be NULL (x must be 16-byte
- *   aligned). Elsewhere the call makes the two launches.
+ *   One launch for fp16 x where the plan is a 4-wavefront tile (32x128, 64x128 or 128x128, split
+ *   or not) and thresh >= 2^-8: the GEMM streams x itself as A, since a row within the threshold
+ *   is its own cast, and computes a tile again, with A rescaled in registers by the rows' exponents,
+ *   only where some |x| of it exceeds the threshold or is NaN (split tiles: the last slice to
+ *   arrive recomputes every slice). Same result bits; no scratch is used. A weight whose call had
+ *   a tile computed again takes the other route below for its next 63 calls when the scratch the
+ *   caller passed allows it (a per-device history in pinned host memory, keyed by w_t).
+ *   One launch for fp32 x where the plan is the unsplit 32x128 tile and K <= 1280: the GEMM's
+ *   workgroups cast their own rows of x into LDS (the rowscale arithmetic, the same bits) and no
+ *   rowscale launch runs; g16_mm_t_scratch_bytes() is then 0 and scratch may be NULL (x must be
+ *   16-byte aligned). Elsewhere the call makes the two launches.
  *   scratch: at least g16_mm_t_scratch_bytes(M, N, K, num_cus) bytes, 16-byte aligned (the fp16
- *   cast and the row scales; it must stay allocated until the GEMM has run).
+ *   cast and the row scales; it must stay allocated until the GEMM has run). It may be NULL on the
+ *   one-launch routes above (fp16 x then always takes the one launch).
  *   workspace / counters: as g16_hgemm_splitk needs them for that ksplit (unused otherwise, then
  *   NULL/0 is fine). thresh: as for the rowscale entry points.
  */
@@ -140,6 +148,10 @@ int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, void* out, i
                   const float* bias, float thresh, int M, int N, int K, int num_cus, void* scratch,
                   size_t scratch_bytes, void* workspace, size_t workspace_bytes, uint32_t* counters,
                   size_t counter_bytes, void* stream);
+/* 1 if the speculation history of the device that owns `stream` routes g16_mm_t_gemm's next call
+ * with this w_t around the one-launch fp16 route (a recent call with it was computed again), else
+ * 0. For tests and diagnostics; no counterpart in the reference. */
+int g16_mm_t_spec_paused(const uint16_t* w_t, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Prepacked weight for the large GEMM (no counterpart kernel in the reference; it serves

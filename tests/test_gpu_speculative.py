@@ -1,15 +1,18 @@
 """One-launch small GEMMs for fp16 activations: on the 4-wavefront tiles (32x128, 64x128, 128x128,
 split or not), g16_mm_t_gemm streams x itself as A. A row whose |max| is within the threshold has
 scale 1, so its rowscale cast is x and the result is exactly the cast path's; where some |x| of a
-tile exceeds the threshold, that tile is computed again from the rescaled cast (in LDS on the
-resident route, else in the scratch buffer; by the last-arriving slice for split tiles).
+tile exceeds the threshold (or is NaN), that tile is computed again with its A fragments rescaled in
+registers, by the rows' exponents taken from the maxima the first pass tracked (by the
+last-arriving slice, over every slice, for split tiles). No scratch buffer is used.
 
 Every case is compared bit for bit with the reference's two-step sequence (rowscale cast, then
 GEMM: ops.py:86-108) run through the separate entry points g16_rowscale_f16 and g16_hgemm_* /
 g16_hgemm_splitk on the same planned route: tiles within the threshold (the streamed path) and
-tiles with rows above it (the recomputation), the threshold's edge, +inf and NaN entries, ragged
-M, N and K, fp16 and fp32 output with and without bias. Also: repeat calls bitwise equal and the
-split counters left zero, the public mm_t, the fp64 oracle, and HIP-graph replays.
+tiles with rows above it (the recomputation), the threshold's edge, +inf and NaN entries (alone
+and in rows that also exceed the threshold), ragged M, N and K, fp16 and fp32 output with and
+without bias, and thresholds from 2^-8 (row exponents up to 24: subnormal factors) to 2^20. Also:
+repeat calls bitwise equal and the split counters left zero, the public mm_t, the fp64 oracle, and
+HIP-graph replays.
 """
 from __future__ import annotations
 
@@ -52,22 +55,21 @@ def _bufs(lib, M, N, K, num_cus, dev):
     return ks, ws, wsb, cnt, cb
 
 
-def _one_launch(lib, x, w, bias, out16, num_cus, bufs):
+def _one_launch(lib, x, w, bias, out16, num_cus, bufs, thresh=1024.0):
+    """g16_mm_t_gemm with no scratch: the speculative route needs none."""
     M, K = x.shape
     N = w.shape[1]
     ks, ws, wsb, cnt, cb = bufs
-    sb = lib.g16_mm_t_scratch_bytes(M, N, K, num_cus)
-    scratch = torch.empty(max(sb, 16), dtype=torch.uint8, device=x.device)
     out = torch.empty(M, N, dtype=torch.float16 if out16 else torch.float32, device=x.device)
     st = lib.g16_mm_t_gemm(x.data_ptr(), 0, w.data_ptr(), out.data_ptr(), 1 if out16 else 0,
-                           None if bias is None else bias.data_ptr(), 1024.0, M, N, K, num_cus,
-                           scratch.data_ptr() if sb else None, sb, ws.data_ptr() if wsb else None, wsb,
+                           None if bias is None else bias.data_ptr(), thresh, M, N, K, num_cus,
+                           None, 0, ws.data_ptr() if wsb else None, wsb,
                            cnt.data_ptr() if cb else None, cb, torch.cuda.current_stream(x.device).cuda_stream)
     assert st == 0, lib.g16_strerror(st)
     return out
 
 
-def _two_launches(lib, x, w, bias, out16, num_cus, bufs):
+def _two_launches(lib, x, w, bias, out16, num_cus, bufs, thresh=1024.0):
     """The reference's sequence through the separate entry points: rowscale, then the GEMM on the
     planned route (split-K where the plan splits)."""
     M, K = x.shape
@@ -77,7 +79,7 @@ def _two_launches(lib, x, w, bias, out16, num_cus, bufs):
     ks, ws, wsb, cnt, cb = bufs
     y = torch.empty(M, K, dtype=torch.float16, device=dev)
     s = torch.empty(M, dtype=torch.float32, device=dev)
-    assert lib.g16_rowscale_f16(x.data_ptr(), y.data_ptr(), s.data_ptr(), M, K, 1024.0, stream) == 0
+    assert lib.g16_rowscale_f16(x.data_ptr(), y.data_ptr(), s.data_ptr(), M, K, thresh, stream) == 0
     out = torch.empty(M, N, dtype=torch.float16 if out16 else torch.float32, device=dev)
     b = None if bias is None else bias.data_ptr()
     if ks > 1:
@@ -91,7 +93,9 @@ def _two_launches(lib, x, w, bias, out16, num_cus, bufs):
 
 def _inputs(M, K, N, kind: str, seed: int, out16: bool):
     """fp16 x: 'within' every |x| <= 1024 (the streamed path); 'over' some rows above it (the
-    recomputation); 'edge' one row at exactly 1024 and one a step above; 'special' +inf and NaN."""
+    recomputation); 'edge' one row at exactly 1024 and one a step above; 'special' +inf and NaN;
+    'nan_over' NaN in a row above the threshold (its exponent comes from its other values) and in
+    a row within it."""
     x = randn((M, K), seed=seed)
     if kind == "over":
         x = outlier_rows(x, 0.1, 2e3, 8e3 if out16 else 6e4, seed=seed + 3)
@@ -103,6 +107,13 @@ def _inputs(M, K, N, kind: str, seed: int, out16: bool):
         x[M // 2, K // 2] = float("inf")
         if M > 2:
             x[1, 0] = float("nan")
+    elif kind == "nan_over":
+        r = M // 2
+        x[r, K - 1] = float("nan")
+        x[r, K // 3] = -2500.0                        # exponent 2 from this entry, NaN dropped
+        x[0, K // 2] = float("nan")                   # a NaN row within the threshold
+        if M > 40:
+            x[40, 3] = -float("nan")
     return x.to(torch.float16), randn((K, N), seed=seed + 1, scale=0.05, dtype=torch.float16)
 
 
@@ -118,7 +129,7 @@ ROUTES = [
     (768, 4056, 4096, 128, 1),    # 128x128 unsplit, ragged K tail
     (40, 8, 136, 32, 1),          # one K step of 8
 ]
-KINDS = ["within", "over", "edge", "special"]
+KINDS = ["within", "over", "edge", "special", "nan_over"]
 
 
 @pytest.mark.parametrize("M,K,N,bm,ks", ROUTES)
@@ -154,6 +165,104 @@ def test_one_launch_equals_the_two_step_sequence_bitwise(lib, cus, cuda, M, K, N
         ref = oracle.mm_t(x.numpy(), w.numpy(), None if bias is None else bias.numpy(),
                           "float16" if out16 else "float32")
         assert oracle.rel_err(one.cpu().numpy(), ref) <= GEMM_TOL
+
+
+# (M, K, N, threshold): the exponents of rows up to 6e4 reach 16 - log2(threshold), 24 at 2^-8
+THRESHOLDS = [
+    (100, 1000, 264, 2.0 ** -8),
+    (64, 4096, 1024, 2.0 ** -8),
+    (1024, 1024, 1024, 2.0 ** -3),
+    (64, 1024, 1024, 1.0),
+    (512, 4096, 4096, 32768.0),
+    (1024, 2048, 1024, 2.0 ** 20),
+]
+
+
+@pytest.mark.parametrize("M,K,N,thresh", THRESHOLDS)
+def test_one_launch_thresholds_bitwise(lib, cus, cuda, M, K, N, thresh):
+    x = randn((M, K), seed=M + N)
+    x = outlier_rows(x, 0.1, 2e3, 6e4, seed=M + 5)
+    x[M // 3, 1] = 65504.0                            # the largest fp16: exponent 16 - log2(thresh)
+    x[M // 3, 2] = 3e-8                               # rounds to an fp16 subnormal, then underflows
+    x16 = x.to(torch.float16)
+    w = randn((K, N), seed=M + 2, scale=0.05, dtype=torch.float16)
+    xd, wd = x16.to(cuda), w.to(cuda)
+    bufs = _bufs(lib, M, N, K, cus, cuda)
+    two = _two_launches(lib, xd, wd, None, False, cus, bufs, thresh)
+    one = _one_launch(lib, xd, wd, None, False, cus, bufs, thresh)
+    torch.cuda.synchronize()
+    assert torch.equal(one.view(torch.int32), two.view(torch.int32))
+    assert int(bufs[3].count_nonzero()) == 0
+
+
+def test_thresholds_below_two_to_minus_8_take_the_two_launch_route(lib, cus, cuda):
+    """2^-9: a row exponent can reach 25, whose factor is below the fp16 range; the library runs the
+    cast and the GEMM as two launches, which need the scratch buffer."""
+    M, K, N = 64, 1024, 1024
+    x16 = randn((M, K), seed=3).to(torch.float16).to(cuda)
+    x16[5, 5] = 60000.0
+    wd = randn((K, N), seed=4, scale=0.05, dtype=torch.float16).to(cuda)
+    bufs = _bufs(lib, M, N, K, cus, cuda)
+    ks, ws, wsb, cnt, cb = bufs
+    out = torch.empty(M, N, device=cuda)
+    stream = torch.cuda.current_stream(cuda).cuda_stream
+    st = lib.g16_mm_t_gemm(x16.data_ptr(), 0, wd.data_ptr(), out.data_ptr(), 0, None, 2.0 ** -9, M, N, K, cus,
+                           None, 0, ws.data_ptr() if wsb else None, wsb, cnt.data_ptr() if cb else None, cb, stream)
+    assert st == -3  # G16_E_NULL: the two-launch route's cast needs the scratch
+    sb = lib.g16_mm_t_scratch_bytes(M, N, K, cus)
+    scratch = torch.empty(sb, dtype=torch.uint8, device=cuda)
+    st = lib.g16_mm_t_gemm(x16.data_ptr(), 0, wd.data_ptr(), out.data_ptr(), 0, None, 2.0 ** -9, M, N, K, cus,
+                           scratch.data_ptr(), sb, ws.data_ptr() if wsb else None, wsb,
+                           cnt.data_ptr() if cb else None, cb, stream)
+    assert st == 0, lib.g16_strerror(st)
+    two = _two_launches(lib, x16, wd, None, False, cus, bufs, 2.0 ** -9)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int32), two.view(torch.int32))
+
+
+def test_a_recomputed_weight_takes_the_other_route_for_63_calls(lib, cus, cuda):
+    """After a call whose tile was computed again, the weight's next 63 calls take the two-launch
+    route (the caller passed the scratch it needs), then speculation resumes; every call's result
+    is the two-step sequence's, bit for bit."""
+    M, K, N = 64, 4096, 1024
+    xo, w = _inputs(M, K, N, "over", seed=11, out16=False)
+    xw, _ = _inputs(M, K, N, "within", seed=12, out16=False)
+    xo, xw, wd = xo.to(cuda), xw.to(cuda), w.to(cuda)
+    bufs = _bufs(lib, M, N, K, cus, cuda)
+    ks, ws, wsb, cnt, cb = bufs
+    stream = torch.cuda.current_stream(cuda).cuda_stream
+    sb = lib.g16_mm_t_scratch_bytes(M, N, K, cus)
+    assert sb > 0
+    scratch = torch.empty(sb, dtype=torch.uint8, device=cuda)
+
+    def call(x):
+        out = torch.empty(M, N, device=cuda)
+        st = lib.g16_mm_t_gemm(x.data_ptr(), 0, wd.data_ptr(), out.data_ptr(), 0, None, 1024.0, M, N, K, cus,
+                               scratch.data_ptr(), sb, ws.data_ptr(), wsb, cnt.data_ptr(), cb, stream)
+        assert st == 0, lib.g16_strerror(st)
+        return out
+
+    ref_o = _two_launches(lib, xo, wd, None, False, cus, bufs)
+    ref_w = _two_launches(lib, xw, wd, None, False, cus, bufs)
+    # leave the slot clear first: calls within the threshold until no pause is left
+    for _ in range(70):
+        call(xw)
+    torch.cuda.synchronize()
+    assert lib.g16_mm_t_spec_paused(wd.data_ptr(), stream) == 0
+    o = call(xo)                      # speculative, computed again: the slot records it
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int32), ref_o.view(torch.int32))
+    assert lib.g16_mm_t_spec_paused(wd.data_ptr(), stream) == 1
+    outs = [call(xo if i % 2 else xw) for i in range(63)]   # the other route: no new miss is noted
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert torch.equal(o.view(torch.int32), (ref_o if i % 2 else ref_w).view(torch.int32))
+    assert lib.g16_mm_t_spec_paused(wd.data_ptr(), stream) == 1
+    o = call(xw)                      # the 64th: speculative again, and within the threshold
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int32), ref_w.view(torch.int32))
+    assert lib.g16_mm_t_spec_paused(wd.data_ptr(), stream) == 0
+    assert int(cnt.count_nonzero()) == 0
 
 
 def test_graph_replays_of_speculative_mm_t_match_eager(cuda):
