@@ -1,11 +1,12 @@
 """One-launch small GEMMs: where mm_t's plan is the unsplit 32x128 tile and K <= 1280,
-g16_mm_t_gemm runs a single GEMM launch whose workgroups cast their own rows of x into LDS (no fp16
-copy in HBM, no rowscale launch). The cast is the rowscale arithmetic and the GEMM the same tile
-and K order, so the result must equal the reference's two-step sequence (rowscale cast, then GEMM:
-ops.py:86-108), run here through the separate entry points g16_rowscale_* and g16_hgemm_*, bit for
-bit -- including rows that are rescaled, +inf and NaN entries, ragged M, N and K, fp16 and fp32
-activations and outputs. Also: repeat calls bitwise equal, the public mm_t on this route, the
-fp64 oracle, and HIP-graph replays.
+g16_mm_t_gemm runs a single GEMM launch and needs no scratch. For fp32 x its workgroups cast their
+own rows of x into LDS (no fp16 copy in HBM, no rowscale launch); for fp16 x it is the speculative
+launch that streams x itself (test_gpu_speculative.py covers it in depth, and the LDS cast of fp16
+x, which the speculation history selects after a recomputation). Either way the result must equal
+the reference's two-step sequence (rowscale cast, then GEMM: ops.py:86-108), run here through the
+separate entry points g16_rowscale_* and g16_hgemm_*, bit for bit -- including rows that are
+rescaled, +inf and NaN entries, ragged M, N and K, fp16 and fp32 activations and outputs. Also:
+repeat calls bitwise equal, the public mm_t on this route, the fp64 oracle, and HIP-graph replays.
 """
 from __future__ import annotations
 

@@ -220,11 +220,12 @@ def test_thresholds_below_two_to_minus_8_take_the_two_launch_route(lib, cus, cud
     assert torch.equal(out.view(torch.int32), two.view(torch.int32))
 
 
-def test_a_recomputed_weight_takes_the_other_route_for_63_calls(lib, cus, cuda):
-    """After a call whose tile was computed again, the weight's next 63 calls take the two-launch
-    route (the caller passed the scratch it needs), then speculation resumes; every call's result
-    is the two-step sequence's, bit for bit."""
-    M, K, N = 64, 4096, 1024
+@pytest.mark.parametrize("M,K,N,with_scratch", [(64, 4096, 1024, True), (1024, 1024, 1024, False)])
+def test_a_recomputed_weight_takes_the_other_route_for_63_calls(lib, cus, cuda, M, K, N, with_scratch):
+    """After a call whose tile was computed again, the weight's next 63 calls take the other route
+    -- the two-launch one where the caller passed the scratch it needs (64x4096x1024), the resident
+    one-launch cast into LDS where the plan allows it (1024^3, no scratch) -- then speculation
+    resumes; every call's result is the two-step sequence's, bit for bit."""
     xo, w = _inputs(M, K, N, "over", seed=11, out16=False)
     xw, _ = _inputs(M, K, N, "within", seed=12, out16=False)
     xo, xw, wd = xo.to(cuda), xw.to(cuda), w.to(cuda)
@@ -232,13 +233,14 @@ def test_a_recomputed_weight_takes_the_other_route_for_63_calls(lib, cus, cuda):
     ks, ws, wsb, cnt, cb = bufs
     stream = torch.cuda.current_stream(cuda).cuda_stream
     sb = lib.g16_mm_t_scratch_bytes(M, N, K, cus)
-    assert sb > 0
-    scratch = torch.empty(sb, dtype=torch.uint8, device=cuda)
+    assert (sb > 0) == with_scratch
+    scratch = torch.empty(max(sb, 16), dtype=torch.uint8, device=cuda)
 
     def call(x):
         out = torch.empty(M, N, device=cuda)
         st = lib.g16_mm_t_gemm(x.data_ptr(), 0, wd.data_ptr(), out.data_ptr(), 0, None, 1024.0, M, N, K, cus,
-                               scratch.data_ptr(), sb, ws.data_ptr(), wsb, cnt.data_ptr(), cb, stream)
+                               scratch.data_ptr() if sb else None, sb, ws.data_ptr() if wsb else None, wsb,
+                               cnt.data_ptr() if cb else None, cb, stream)
         assert st == 0, lib.g16_strerror(st)
         return out
 
@@ -263,6 +265,20 @@ def test_a_recomputed_weight_takes_the_other_route_for_63_calls(lib, cus, cuda):
     assert torch.equal(o.view(torch.int32), ref_w.view(torch.int32))
     assert lib.g16_mm_t_spec_paused(wd.data_ptr(), stream) == 0
     assert int(cnt.count_nonzero()) == 0
+
+
+def test_without_scratch_a_split_shape_always_speculates(lib, cus, cuda):
+    """No scratch and no resident plan: the two-launch route is not available, so a weight whose call
+    was computed again keeps the one-launch route (and its result bits)."""
+    M, K, N = 64, 1024, 1024
+    xo, w = _inputs(M, K, N, "over", seed=21, out16=False)
+    xo, wd = xo.to(cuda), w.to(cuda)
+    bufs = _bufs(lib, M, N, K, cus, cuda)
+    ref = _two_launches(lib, xo, wd, None, False, cus, bufs)
+    outs = [_one_launch(lib, xo, wd, None, False, cus, bufs) for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o.view(torch.int32), ref.view(torch.int32))
 
 
 def test_graph_replays_of_speculative_mm_t_match_eager(cuda):
