@@ -978,7 +978,19 @@ struct Plan {
   Tile tile;
   int bm, bn;
   int ntm, ntn;
+  int ks = 0;  // the split the tile was chosen with (the modelled choice below); 0: the planner's rule
 };
+
+struct KSplit {
+  int ksplit;
+  int kchunk;
+};
+
+KSplit ksplit_for(int K, int ksplit) {
+  if (K <= 0 || ksplit <= 1) return {1, K > 0 ? K : 0};
+  const int kchunk = ceil_div(ceil_div(K, ksplit), kSplitAlign) * kSplitAlign;
+  return {ceil_div(K, kchunk), kchunk};
+}
 
 // Compute units of device `dev` (cached per device; 256, the MI355X count, if the query fails).
 int cus_of_device(int dev) {
@@ -1015,18 +1027,64 @@ int current_cus() {
 constexpr int kMaxK = G16_GEMM_MAX_K;
 constexpr int kMaxN = G16_GEMM_MAX_N;
 
-// The same tile with or without a split: a split only spreads K over more workgroups. Large
-// outputs take the 256x256 tile once it gives more than half the CUs a workgroup; just below that
-// (3/8 to 1/2 of the CUs), the 256x128 tile on the same schedule fills them instead (2048 x 4096^2,
-// 128 tiles of 256^2 on 256 CUs: 89 us, 256 tiles of 256x128: 76-82 us; with 144 tiles of 256^2
-// the 256x128 grid would overflow the CUs: 93 vs 128 us). Below that, with K <= 3072, the
-// 4-wavefront tile with the most tiles that still fit one round on the CUs (32x128, then 64x128,
-// else 128x128): a small GEMM is bound by how many CUs it occupies (graph-timed, 256 CUs, M x N x K:
-// 1024^3 13.7 us on 128^2 tiles, 10.3 on 64x128, 8.9 on 32x128; 768 x 1024^2 13.4 -> 8.6;
-// 512 x 3072 x 1024 14.5 -> 11.2 on 64x128, where 32x128 tiles would need 1.5 rounds;
-// 1024 x 3072 x 768 stays on 128^2, 14.4 against 16.1-17.5; 256 x 1024 x 3072 16-19 -> 9.6 split
-// 4 ways; 1024 x 1024 x 3072 22 -> 19). At K = 4096 the 128^2 tile with a split wins or ties
-// (512 x 4096^2 30.0 us against 31.2 on 64x128 and 37.3 on 32x128).
+// Tile and split of the 4-wavefront tiles (32x128, 64x128, 128x128) for M > 64 outside the
+// 256-row tiles' range: the pair with the least modelled time among those whose grid fits one round
+// on the CUs (1 to 8 slices of >= 256 K). Per tile, time (us) = a + b * KB + c * T + [split] * (d
+// + e * P + f * g / CUs) + h * [tiles % 8 != 0] * T, where KB = the A and B bytes one workgroup
+// streams, (BM + 128) * kchunk * 2 / 1024; g = workgroups (tiles x slices); T = g * KB / 1024, the
+// grid's traffic; P = the KB of fp32 partial tiles the last slice reads back; and the last term is
+// the traffic without the XCD-grouped tile order (which needs the tile count to be a multiple of
+// 8: each XCD's L2 then serves its own panels). Least-squares fit of graph-timed kernels on 256
+// CUs: 148 shapes, M = 72..1024, K = 264..14336, N = 264..14336, every tile and split that fits one
+// round. Fitted on one half of the shapes, its picks on the other half took 1.5 % more time than
+// the best measured pairs (40 random halvings; at most 1.7 %). The rule it replaces (the 32- and
+// 64-row tiles only for K <= 3072) took 7.8 % more over the same shapes and up to 2x on some, e.g.
+// 192 x 4096 x 512: 18.0 us on 128x128 tiles split 4 ways against 9.4 on 32x128 split 8 ways;
+// 96 x 14336 x 1024: 27.4 vs 15.1; 128 x 4096^2: 20.2 vs 15.8 on 64x128 split 4 ways.
+struct TileCost {
+  Tile tile;
+  int bm;
+  double a, b, c, d, e, f, h;
+};
+constexpr TileCost kTileCost[3] = {
+    {Tile::T32, 32, 4.6486, 0.010806, 0.013869, 0.74353, 0.012399, 1.1007, 0.036118},
+    {Tile::T64, 64, 5.7715, 0.010761, 0.019761, 0.46654, 0.012608, 2.0929, 0.028632},
+    {Tile::T128, 128, 6.6612, 0.013002, 0.019072, 0.32533, 0.013334, 3.4585, 0.014512},
+};
+
+bool modelled_tile(int M, int N, int K, int num_cus, Plan& out) {
+  double best = 0.0;
+  bool found = false;
+  for (const TileCost& c : kTileCost) {
+    const long tiles = static_cast<long>(ceil_div(M, c.bm)) * ceil_div(N, 128);
+    for (int want = 1; want <= 8; ++want) {
+      if (want > 1 && K / want < 256) break;
+      const KSplit sp = ksplit_for(K, want);
+      if (sp.ksplit != want) continue;  // fewer slices than asked: counted at that count
+      const long g = tiles * sp.ksplit;
+      if (g > num_cus) break;
+      const double kb = (c.bm + 128) * static_cast<double>(sp.kchunk) * 2.0 / 1024.0;
+      const double traffic = static_cast<double>(g) * kb / 1024.0;
+      const double part = sp.ksplit * c.bm * 128 * 4 / 1024.0;
+      double t = c.a + c.b * kb + c.c * traffic + (tiles % 8 != 0 ? c.h * traffic : 0.0);
+      if (sp.ksplit > 1) t += c.d + c.e * part + c.f * static_cast<double>(g) / num_cus;
+      if (!found || t < best) {
+        best = t;
+        out = Plan{c.tile, c.bm, 128, ceil_div(M, c.bm), ceil_div(N, 128), sp.ksplit};
+        found = true;
+      }
+    }
+  }
+  return found;
+}
+
+// The same tile with or without a split: a split only spreads K over more workgroups. M <= 64 takes
+// the 32x128 or 64x128 tile (below). Large outputs take the 256x256 tile once it gives more than
+// half the CUs a workgroup; just below that (3/8 to 1/2 of the CUs), the 256x128 tile on the same
+// schedule fills them instead (2048 x 4096^2, 128 tiles of 256^2 on 256 CUs: 89 us, 256 tiles of
+// 256x128: 76-82 us; with 144 tiles of 256^2 the 256x128 grid would overflow the CUs: 93 vs 128 us).
+// Below that, the modelled 4-wavefront choice above; where no 4-wavefront grid fits one round, the
+// 128x128 tile unsplit.
 Plan choose_tile(int M, int N, int K, int num_cus) {
   Plan p{};
   const long t256 = static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256);
@@ -1042,27 +1100,14 @@ Plan choose_tile(int M, int N, int K, int num_cus) {
     p.tile = Tile::T256; p.bm = 256; p.bn = 256;
   } else if (M >= 1024 && N >= 256 && 8 * t256 > 3 * num_cus) {
     p.tile = Tile::T256N; p.bm = 256; p.bn = 128;
-  } else if (K <= 3072 && static_cast<long>(ceil_div(M, 32)) * ceil_div(N, 128) <= num_cus) {
-    p.tile = Tile::T32; p.bm = 32; p.bn = 128;
-  } else if (K <= 3072 && static_cast<long>(ceil_div(M, 64)) * ceil_div(N, 128) <= num_cus) {
-    p.tile = Tile::T64; p.bm = 64; p.bn = 128;
+  } else if (modelled_tile(M, N, K, num_cus, p)) {
+    return p;
   } else {
     p.tile = Tile::T128; p.bm = 128; p.bn = 128;
   }
   p.ntm = ceil_div(M, p.bm);
   p.ntn = ceil_div(N, p.bn);
   return p;
-}
-
-struct KSplit {
-  int ksplit;
-  int kchunk;
-};
-
-KSplit ksplit_for(int K, int ksplit) {
-  if (K <= 0 || ksplit <= 1) return {1, K > 0 ? K : 0};
-  const int kchunk = ceil_div(ceil_div(K, ksplit), kSplitAlign) * kSplitAlign;
-  return {ceil_div(K, kchunk), kchunk};
 }
 
 template <bool OUT_F16>
@@ -1216,6 +1261,7 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   // 512 x 4096^2: 128 tiles unsplit 44 us, 2 slices 36 us; 512 x 11008 x 4096: 104 vs 75 us).
   if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0) return 1;
   const g16::Plan q = g16::choose_tile(M, N, K, num_cus);
+  if (q.ks > 0) return q.ks;  // chosen with its tile (modelled_tile)
   const int tiles = q.ntm * q.ntn;
   if (tiles >= num_cus || K < 512) return 1;
   // At most 8 slices: the last slice to arrive reads every other slice's fp32 tile at one CU's

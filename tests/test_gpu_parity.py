@@ -134,8 +134,8 @@ SHAPES = [  # (M, K, N) -- reference sweep, tests/test_correctness.py:14-18
 ]
 
 
-# Medium shapes with K <= 3072 run on the 32x128 or 64x128 tile whose grid fills one round of the
-# CUs (unsplit, or split where the tiles still leave CUs idle); bitwise repeatable either way.
+# Medium shapes run on the 32x128 or 64x128 tile, unsplit or split, as the planner's model picks
+# them (here all within one round of the CUs); bitwise repeatable either way.
 @pytest.mark.parametrize("M,K,N", [(256, 3072, 1024), (1024, 3072, 1024), (520, 2056, 3072), (1024, 1024, 1024)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 def test_short_k_small_tiles_match_oracle(g, cuda, M, K, N, out_dtype):
@@ -538,7 +538,7 @@ def test_skinny_partial_block_ignores_rows_past_the_slice(lib, cuda, M, K, N, ks
     assert oracle.rel_err(y[:, finite], ref[:, finite]) <= SKINNY_TOL
 
 
-# One shape per route of the GEMM path: plain 128x128 tiles, split-K, tile-packed 256x256, tile-packed
+# One shape per route of the GEMM path: plain 32x128 tiles, split-K, tile-packed 256x256, tile-packed
 # 256x128 (128 tiles of 256^2 would leave half the CUs idle)
 @pytest.mark.parametrize("M,K,N", [(300, 136, 264), (64, 1024, 1024), (4100, 264, 2056), (2048, 264, 4096)])
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.float16])

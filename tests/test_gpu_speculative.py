@@ -125,7 +125,9 @@ ROUTES = [
     (1024, 2048, 1024, 32, 1),    # unsplit 32x128 past the resident K: recomputes from the scratch
     (100, 1000, 264, 32, 3),      # ragged M, N, K
     (64, 4096, 11008, 64, 2),     # 64x128 split twice
-    (512, 4096, 4096, 128, 2),    # 128x128 split twice
+    (128, 4096, 4096, 64, 4),     # 64x128 split 4 ways
+    (192, 4096, 512, 32, 8),      # 32x128 split 8 ways at M > 64
+    (128, 4096, 11008, 128, 2),   # 128x128 split twice
     (768, 4056, 4096, 128, 1),    # 128x128 unsplit, ragged K tail
     (40, 8, 136, 32, 1),          # one K step of 8
 ]
