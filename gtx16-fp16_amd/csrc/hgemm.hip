@@ -246,9 +246,19 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   const uint32_t sA_lds = lds_base(&sA[0][0]), sB_lds = lds_base(&sB[0][0]);
 
   // ---- tile assignment (XCD-aware, grouped) ----
+  // Workgroups reach the 8 XCDs round-robin by linear index. Each XCD's workgroups get a contiguous
+  // range of the grouped tile order below, so its L2 serves a compact block of tile rows and
+  // columns: ranges of ntiles / 8 tiles; with an unsplit grid of another size, ranges of
+  // floor(ntiles / 8) or one more. (For split grids of such sizes the linear order is kept: a
+  // slice-major mapping measured 1-3 us slower there.)
   const int ntiles = ntm * ntn;
   int lin = blockIdx.x;
-  if (ntiles % 8 == 0) lin = (lin % 8) * (ntiles / 8) + lin / 8;
+  if (ntiles % 8 == 0) {
+    lin = (lin % 8) * (ntiles / 8) + lin / 8;
+  } else if (gridDim.y == 1) {
+    const int xcd = lin % 8, q8 = ntiles / 8, r8 = ntiles % 8;
+    lin = xcd * q8 + min(xcd, r8) + lin / 8;  // XCD x holds q8 + (x < r8) workgroups
+  }
   const int per_group = kGroupM * ntn;
   const int first_m = (lin / per_group) * kGroupM;
   const int gsz = min(ntm - first_m, kGroupM);
@@ -1030,14 +1040,14 @@ constexpr int kMaxN = G16_GEMM_MAX_N;
 // Tile and split of the 4-wavefront tiles (32x128, 64x128, 128x128) for M > 64 outside the
 // 256-row tiles' range: the pair with the least modelled time among those whose grid fits one round
 // on the CUs (1 to 8 slices of >= 256 K). Per tile, time (us) = a + b * KB + c * T + [split] * (d
-// + e * P + f * g / CUs) + h * [tiles % 8 != 0] * T, where KB = the A and B bytes one workgroup
+// + e * P + f * g / CUs + h * [tiles % 8 != 0] * T), where KB = the A and B bytes one workgroup
 // streams, (BM + 128) * kchunk * 2 / 1024; g = workgroups (tiles x slices); T = g * KB / 1024, the
-// grid's traffic; P = the KB of fp32 partial tiles the last slice reads back; and the last term is
-// the traffic without the XCD-grouped tile order (which needs the tile count to be a multiple of
-// 8: each XCD's L2 then serves its own panels). Least-squares fit of graph-timed kernels on 256
-// CUs: 148 shapes, M = 72..1024, K = 264..14336, N = 264..14336, every tile and split that fits one
-// round. Fitted on one half of the shapes, its picks on the other half took 1.5 % more time than
-// the best measured pairs (40 random halvings; at most 1.7 %). The rule it replaces (the 32- and
+// grid's traffic; P = the KB of fp32 partial tiles the last slice reads back; and the h term is the
+// traffic of a split grid without the XCD-grouped tile order (which split grids get only when the
+// tile count is a multiple of 8). Least-squares fit of graph-timed kernels on 256 CUs: 148
+// shapes, M = 72..1024, K = 264..14336, N = 264..14336, every tile and split that fits one round.
+// Fitted on one half of the shapes, its picks on the other half took 1.1 % more time than the best
+// measured pairs (40 random halvings; at most 1.7 %). The rule it replaces (the 32- and
 // 64-row tiles only for K <= 3072) took 7.8 % more over the same shapes and up to 2x on some, e.g.
 // 192 x 4096 x 512: 18.0 us on 128x128 tiles split 4 ways against 9.4 on 32x128 split 8 ways;
 // 96 x 14336 x 1024: 27.4 vs 15.1; 128 x 4096^2: 20.2 vs 15.8 on 64x128 split 4 ways.
@@ -1047,9 +1057,9 @@ struct TileCost {
   double a, b, c, d, e, f, h;
 };
 constexpr TileCost kTileCost[3] = {
-    {Tile::T32, 32, 4.6486, 0.010806, 0.013869, 0.74353, 0.012399, 1.1007, 0.036118},
-    {Tile::T64, 64, 5.7715, 0.010761, 0.019761, 0.46654, 0.012608, 2.0929, 0.028632},
-    {Tile::T128, 128, 6.6612, 0.013002, 0.019072, 0.32533, 0.013334, 3.4585, 0.014512},
+    {Tile::T32, 32, 4.6481, 0.011181, 0.013789, 0.36365, 0.013646, 0.97333, 0.044944},
+    {Tile::T64, 64, 6.0134, 0.010972, 0.01919, -0.068908, 0.012927, 1.9405, 0.040133},
+    {Tile::T128, 128, 6.7721, 0.012987, 0.019247, 0.29649, 0.01301, 3.4194, 0.014194},
 };
 
 bool modelled_tile(int M, int N, int K, int num_cus, Plan& out) {
@@ -1066,8 +1076,9 @@ bool modelled_tile(int M, int N, int K, int num_cus, Plan& out) {
       const double kb = (c.bm + 128) * static_cast<double>(sp.kchunk) * 2.0 / 1024.0;
       const double traffic = static_cast<double>(g) * kb / 1024.0;
       const double part = sp.ksplit * c.bm * 128 * 4 / 1024.0;
-      double t = c.a + c.b * kb + c.c * traffic + (tiles % 8 != 0 ? c.h * traffic : 0.0);
-      if (sp.ksplit > 1) t += c.d + c.e * part + c.f * static_cast<double>(g) / num_cus;
+      double t = c.a + c.b * kb + c.c * traffic;
+      if (sp.ksplit > 1)
+        t += c.d + c.e * part + c.f * static_cast<double>(g) / num_cus + (tiles % 8 != 0 ? c.h * traffic : 0.0);
       if (!found || t < best) {
         best = t;
         out = Plan{c.tile, c.bm, 128, ceil_div(M, c.bm), ceil_div(N, 128), sp.ksplit};

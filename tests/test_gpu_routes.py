@@ -83,12 +83,12 @@ def test_c1_matmul_exactly_as_configured(g, cuda):
 ROUTES = [
     (64, 1024, 1024, (32, 128), 4),      # C3
     (64, 4096, 1024, (32, 128), 8),      # C3
-    (128, 4096, 11008, (128, 128), 2),   # 128x128 split twice
+    (384, 4096, 4096, (128, 128), 2),    # 128x128 split twice
     (64, 4096, 11008, (64, 128), 2),     # 64x128 split twice
     (128, 4096, 4096, (64, 128), 4),     # 64x128 split 4 ways at M > 64
     (192, 4096, 512, (32, 128), 8),      # 32x128 split 8 ways at M > 64
     (768, 4056, 4096, (128, 128), 1),    # 128x128 unsplit: 127 K steps, the last one ragged
-    (128, 4056, 11008, (128, 128), 2),   # split: slices of 64 and 63 K steps, the last one ragged
+    (384, 4056, 3072, (128, 128), 3),    # split: slices of 44, 44 and 39 K steps, the last one ragged
 ]
 
 

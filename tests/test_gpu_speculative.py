@@ -127,7 +127,8 @@ ROUTES = [
     (64, 4096, 11008, 64, 2),     # 64x128 split twice
     (128, 4096, 4096, 64, 4),     # 64x128 split 4 ways
     (192, 4096, 512, 32, 8),      # 32x128 split 8 ways at M > 64
-    (128, 4096, 11008, 128, 2),   # 128x128 split twice
+    (384, 4096, 4096, 128, 2),    # 128x128 split twice
+    (384, 4056, 3072, 128, 3),    # 128x128 split 3 ways, ragged last K step
     (768, 4056, 4096, 128, 1),    # 128x128 unsplit, ragged K tail
     (40, 8, 136, 32, 1),          # one K step of 8
 ]
