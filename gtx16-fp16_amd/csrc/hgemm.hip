@@ -65,6 +65,10 @@ namespace {
 
 constexpr int kGroupM = 8;
 constexpr int kSplitAlign = 64;  // split-K slices start on a multiple of every tile's K step
+// The planner's rule (M <= 64) splits no K below this: two slices of 256 cost more than they save
+// (graph-timed: 16 x 8192 x 512 (M x N x K) 6.0 us unsplit, 7.1 split twice; 48 x 2048 x 512 6.2
+// vs 7.2); at K = 1024 four slices win (64 x 1024^2 7.7 -> 7.1).
+constexpr int kMinSplitK = 1024;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every descriptor's range: reads 0
 
 typedef short short4v __attribute__((ext_vector_type(4)));
@@ -1099,11 +1103,14 @@ bool modelled_tile(int M, int N, int K, int num_cus, Plan& out) {
 Plan choose_tile(int M, int N, int K, int num_cus) {
   Plan p{};
   const long t256 = static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 256);
-  if (M <= 32 || (M <= 64 && 4L * ceil_div(N, 128) <= num_cus)) {
+  if (M <= 32 || (M <= 64 && 4L * ceil_div(N, 128) <= num_cus) ||
+      (M <= 64 && K < kMinSplitK && 2L * ceil_div(N, 128) <= num_cus)) {
     // M = 33..64 on two rows of 32x128 tiles while they fill at most half the CUs, so the split
     // still doubles them (graph-timed, M x N x K: 64 x 1024^2 8.6 -> 6.8 us, 64 x 1024 x 4096
     // 11.4 -> 9.7, 64 x 4096^2 13.9 -> 11.9, 64 x 4096 x 11008 23.6 -> 21.5); with more tiles than
-    // that, 64x128 tiles split twice beat unsplit 32x128 ones (64 x 11008 x 4096: 21.4 vs 31.3 us).
+    // that, 64x128 tiles split twice beat unsplit 32x128 ones (64 x 11008 x 4096: 21.4 vs 31.3 us),
+    // except at K below kMinSplitK, which is not split: then 32x128 tiles wherever their grid fits
+    // one round (40 x 11008 x 512: 6.6 us against 9.7 on 64x128 tiles split twice).
     p.tile = Tile::T32; p.bm = 32; p.bn = 128;
   } else if (M <= 64) {
     p.tile = Tile::T64; p.bm = 64; p.bn = 128;
@@ -1274,7 +1281,7 @@ extern "C" int g16_hgemm_plan(int M, int N, int K, int num_cus) {
   const g16::Plan q = g16::choose_tile(M, N, K, num_cus);
   if (q.ks > 0) return q.ks;  // chosen with its tile (modelled_tile)
   const int tiles = q.ntm * q.ntn;
-  if (tiles >= num_cus || K < 512) return 1;
+  if (tiles >= num_cus || K < g16::kMinSplitK) return 1;
   // At most 8 slices: the last slice to arrive reads every other slice's fp32 tile at one CU's
   // bandwidth, so beyond ~8 the reduction costs more than the extra parallelism gains (measured:
   // 64x4096x1024 12.1 us at 8 vs 14.3 us at 16). Each slice keeps >= 256 K (>= 1024 K for the

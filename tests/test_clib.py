@@ -160,9 +160,10 @@ def test_plans_and_buffer_sizes(lib):
 def test_one_launch_route_needs_no_scratch(lib):
     # mm_t's GEMM path is one launch (the cast in LDS, no scratch) exactly where the plan is the
     # unsplit 32x128 tile and K <= 1280
-    for M, N, K in [(1024, 1024, 1024), (1000, 1000, 1000), (1024, 1024, 1280), (20, 1024, 256), (1000, 1024, 8)]:
+    for M, N, K in [(1024, 1024, 1024), (1000, 1000, 1000), (1024, 1024, 1280), (20, 1024, 256), (20, 1024, 512),
+                    (1000, 1024, 8)]:
         assert lib.g16_mm_t_scratch_bytes(M, N, K, 256) == 0, (M, N, K)
-    for M, N, K in [(1024, 1024, 1288), (1024, 1024, 2048), (20, 1024, 512), (64, 1024, 1024), (4096, 4096, 4096)]:
+    for M, N, K in [(1024, 1024, 1288), (1024, 1024, 2048), (20, 1024, 1024), (64, 1024, 1024), (4096, 4096, 4096)]:
         assert lib.g16_mm_t_scratch_bytes(M, N, K, 256) > 0, (M, N, K)
 
 
