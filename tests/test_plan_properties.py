@@ -30,8 +30,9 @@ def _tile(lib, M: int, N: int, K: int, num_cus: int) -> tuple[int, int, int]:
     """(rows, columns, count) of the tile the library runs this shape on for num_cus CUs, read
     from the library's own size queries for a 2-way split (the tile does not depend on the split):
     the counters hold one 256-byte line per tile and the partials 2 slices x tile x 4 bytes. (Split
-    slices start on multiples of 64 K, so K < 128 cannot split; the tile rules treat every K up
-    to 3072 alike, so those shapes are asked about at K = 128.)"""
+    slices start on multiples of 64 K, so K < 128 cannot split; those shapes are asked about at
+    K = 128, which plans the same tile: below 512 K nothing splits, and the smallest 4-wavefront
+    tile whose grid fits one round wins.)"""
     Kq = max(K, 128)
     ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
     area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
@@ -58,6 +59,9 @@ def test_gemm_plan_limits(lib, M, N, K, num_cus):
     # the packed route is exactly the unsplit 256-row tiles (their packed stage images)
     assert lib.g16_hgemm_use_packed(M, N, K, num_cus) == (1 if (bm == 256 and ks == 1) else 0)
     assert 1 <= ks <= 8
+    # the 4-wavefront tiles' grid fits one round of the CUs whenever one of them can
+    if 32 < M and bm < 256 and min(_ceil(M, r) * _ceil(N, 128) for r in (32, 64, 128)) <= num_cus:
+        assert tiles * ks <= num_cus
     if ks > 1:
         # split only when tiles leave CUs idle, never past one workgroup per CU, >= 256 K a slice
         assert tiles < num_cus
