@@ -140,7 +140,8 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_hgemm_use_packed(2048, 4096, 4096, 256) == 1
     assert lib.g16_hgemm_use_packed_b(2048, 4096, 4096, 256) == 1
     assert lib.g16_hgemm_use_packed_b(4096, 4096, 4096, 256) == 1
-    assert lib.g16_hgemm_use_packed_b(1536, 4096, 4096, 256) == 0    # 128x128 tiles, not packed
+    assert lib.g16_hgemm_use_packed_b(1536, 4096, 4096, 256) == 1    # 128x128 tiles would need 1.5 rounds
+    assert lib.g16_hgemm_use_packed_b(1536, 4096, 1024, 256) == 0    # short K: 128x128 tiles, not packed
     # skinny: 256-column strips up to N = 8192, 512 above; whole 16-row blocks per wavefront, at
     # most one workgroup per CU
     assert lib.g16_skinny_strip_cols(1, 4096) == 256 and lib.g16_skinny_strip_cols(8, 8192) == 256
