@@ -52,9 +52,9 @@ def test_gemm_plan_limits(lib, M, N, K, num_cus):
     # one of the compiled tiles, covering the output exactly once
     assert (bm, bn) in TILES
     assert tiles == _ceil(M, bm) * _ceil(N, bn)
-    # a 256-row tile only where the rows fill it at least 4 times over; tiles never taller than
+    # a 256-row tile only where the rows fill it at least twice over; tiles never taller than
     # needed below that (32-row tiles serve M <= 32)
-    assert bm < 256 or M >= 1024
+    assert bm < 256 or M >= 512
     assert M > 32 or bm == 32
     # the packed route is exactly the unsplit 256-row tiles (their packed stage images)
     assert lib.g16_hgemm_use_packed(M, N, K, num_cus) == (1 if (bm == 256 and ks == 1) else 0)
