@@ -1120,17 +1120,19 @@ Plan choose_tile(int M, int N, int K, int num_cus) {
     p.tile = Tile::T256N; p.bm = 256; p.bn = 128;
   } else if (modelled_tile(M, N, K, num_cus, p)) {
     return p;
-  } else if (M >= 512 && N >= 256 && K >= 4096 && 5L * ceil_div(M, 256) * 256 <= 6L * M) {
-    // No 4-wavefront grid fits one round: with long K the 256-row tiles on their packed route win
-    // over 128x128 tiles that need 1.25 rounds or more -- the 256x128 tile where its grid fits one
-    // round, else the 256x256 one (mm_t, fp32 x, graph-timed, M x N x K: 1280 x 4096^2 78.9 -> 72.9
-    // us, 1536 x 4096^2 81.6 -> 77.2, 1280 x 4096 x 11008 210 -> 181; plain kernels: 512 x 11008 x
-    // 4096 74.5 -> 68.1, 768 x 8192^2 146.6 -> 127.3 (256x128), 768 x 11008 x 4096 116.9 -> 91.6,
-    // 640 x 14336 x 4096 121.1 -> 90.0 (256x256)). Not where the last tile row would be mostly
-    // padding (more than 1/5 of the rows: 600 x 11008 x 4096, fp16 x, 92.7 -> 97.6), nor with
-    // short K (1100 x 4096 x 264: 17.5 -> 18.5); fp16 x at K = 4096 loses a little too, since its
-    // one-launch route needs a 4-wavefront tile (1280 x 4096^2: 69.8 -> 72.7).
-    if (static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 128) <= num_cus) {
+  } else if (M >= 512 && N >= 256 && K >= 1024 && 5L * ceil_div(M, 256) * 256 <= 6L * M &&
+             (K >= 4096 || static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 128) > num_cus)) {
+    // No 4-wavefront grid fits one round: the 256-row tiles on their packed route win over 128x128
+    // tiles that need 1.25 rounds or more -- the 256x128 tile where its grid fits one round and K
+    // is long, else the 256x256 one (mm_t, fp32 x, graph-timed, M x N x K: 1280 x 4096^2 78.9 ->
+    // 72.9 us, 1280 x 4096 x 11008 210 -> 181 on 256x128; 768 x 11008 x 4096 126.7 -> 96.0, 640 x
+    // 14336 x 4096 117.8 -> 97.2 on 256x256; plain kernels at short K: 768 x 11008 x 2048 61.7 ->
+    // 54.6, 768 x 11008 x 3072 87.3 -> 71.2, 640 x 14336 x 2048 61.6 -> 54.6 on 256x256, while 256x128
+    // tiles lose or tie there: 1280 x 4096 x 2048 39.7 vs 40.5). Not where more than a fifth of the
+    // last tile row would be padding (600 x 11008 x 4096, fp16 x, 92.7 -> 97.6), nor below K =
+    // 1024 (1100 x 4096 x 264: 17.5 -> 18.5 on 256x128); fp16 x at K = 4096 loses a little, since
+    // its one-launch route needs a 4-wavefront tile (1280 x 4096^2: 69.8 -> 72.7).
+    if (K >= 4096 && static_cast<long>(ceil_div(M, 256)) * ceil_div(N, 128) <= num_cus) {
       p.tile = Tile::T256N; p.bm = 256; p.bn = 128;
     } else {
       p.tile = Tile::T256; p.bm = 256; p.bn = 256;
