@@ -1403,11 +1403,12 @@ bool mm_t_resident(int M, int N, int K, int num_cus) {
   return resident_route(choose_tile(M, N, K, num_cus), ksplit_for(K, g16_hgemm_plan(M, N, K, num_cus)).ksplit, K);
 }
 
-// Speculation history, per device: a speculative launch that had to compute a tile again stores 1
-// into its weight's slot (pinned host memory, written by the kernel). g16_mm_t_gemm then sends the
-// weight's next kSpecRetry - 1 calls down the resident or two-launch route (the same result bits,
-// without the recomputation) and speculates again after that. Weights whose pointers hash alike
-// share a slot; the route never changes a result, only its time.
+// Speculation history, per device, once g16_mm_t_spec_history has enabled it: a speculative launch
+// that had to compute a tile again stores 1 into its weight's slot (pinned host memory, written by
+// the kernel). g16_mm_t_gemm then sends the weight's next kSpecRetry - 1 calls down the resident or
+// two-launch route (the same result bits, without the recomputation) and speculates again after
+// that. Weights whose pointers hash alike share a slot; the route never changes a result, only its
+// time.
 constexpr int kSpecSlots = 1024;
 constexpr uint32_t kSpecRetry = 64;
 struct SpecHistory {
@@ -1421,35 +1422,23 @@ size_t spec_slot(const void* w_t) {
 }
 static_assert(kSpecSlots == 1024, "spec_slot keeps 10 bits");
 
-// The history of the device that owns `stream`, allocated on first use; NULL while that stream is
-// being captured into a graph before then (no allocation during a capture) or if allocation fails.
-SpecHistory* spec_history(hipStream_t stream) {
-  static std::atomic<SpecHistory*> hist[64];
-  static std::mutex mu;
+// The histories, per device, once g16_mm_t_spec_history has allocated them (the GEMM entry points
+// themselves never allocate).
+std::atomic<SpecHistory*> g_spec_hist[64];
+std::mutex g_spec_mu;
+
+int stream_device(hipStream_t stream) {
   int dev = 0;
   if (stream == nullptr || hipStreamGetDevice(stream, &dev) != hipSuccess) {
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
   }
-  if (dev < 0 || dev >= 64) return nullptr;
-  SpecHistory* h = hist[dev].load(std::memory_order_acquire);
-  if (h != nullptr) return h;
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (stream != nullptr && (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone))
-    return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  h = hist[dev].load(std::memory_order_acquire);
-  if (h != nullptr) return h;
-  void* p = nullptr;
-  if (hipHostMalloc(&p, kSpecSlots * sizeof(uint32_t), hipHostMallocPortable | hipHostMallocCoherent) != hipSuccess) {
-    (void)hipGetLastError();  // leave no error behind for the caller's next check
-    return nullptr;
-  }
-  __builtin_memset(p, 0, kSpecSlots * sizeof(uint32_t));
-  h = new SpecHistory;
-  h->miss = static_cast<uint32_t*>(p);
-  for (auto& r : h->routed) r.store(0, std::memory_order_relaxed);
-  hist[dev].store(h, std::memory_order_release);
-  return h;
+  return dev >= 0 && dev < 64 ? dev : -1;
+}
+
+// The history of the device that owns `stream`, or NULL if it has none.
+SpecHistory* spec_history(hipStream_t stream) {
+  const int dev = stream_device(stream);
+  return dev < 0 ? nullptr : g_spec_hist[dev].load(std::memory_order_acquire);
 }
 
 // fp16 x runs as one speculative launch wherever the plan is a 4-wavefront tile.
@@ -1541,6 +1530,34 @@ extern "C" int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, v
   const int ks = g16_hgemm_plan(M, N, K, num_cus);
   return g16::gemm_launch(y, w_t, out, out_is_f16 != 0, bias, s, M, N, K, ks, num_cus, workspace, workspace_bytes,
                           counters, counter_bytes, stream);
+}
+
+extern "C" int g16_mm_t_spec_history(void* stream) {
+  // once per device: the pinned words the speculative launches report recomputations into
+  const int dev = g16::stream_device(static_cast<hipStream_t>(stream));
+  if (dev < 0) return G16_E_NULL;
+  if (g16::g_spec_hist[dev].load(std::memory_order_acquire) != nullptr) return G16_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (stream != nullptr) {
+    const hipError_t e = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (cap != hipStreamCaptureStatusNone) return static_cast<int>(hipErrorStreamCaptureUnsupported);
+  }
+  std::lock_guard<std::mutex> lock(g16::g_spec_mu);
+  if (g16::g_spec_hist[dev].load(std::memory_order_acquire) != nullptr) return G16_OK;
+  g16::StreamDeviceScope on_device(static_cast<hipStream_t>(stream));
+  void* p = nullptr;
+  const hipError_t e = hipHostMalloc(&p, g16::kSpecSlots * sizeof(uint32_t), hipHostMallocPortable | hipHostMallocCoherent);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // reported here; leave no sticky error behind
+    return static_cast<int>(e);
+  }
+  __builtin_memset(p, 0, g16::kSpecSlots * sizeof(uint32_t));
+  auto* h = new g16::SpecHistory;
+  h->miss = static_cast<uint32_t*>(p);
+  for (auto& r : h->routed) r.store(0, std::memory_order_relaxed);
+  g16::g_spec_hist[dev].store(h, std::memory_order_release);
+  return G16_OK;
 }
 
 extern "C" int g16_mm_t_spec_paused(const uint16_t* w_t, void* stream) {

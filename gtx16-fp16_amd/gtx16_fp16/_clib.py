@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before libg16.so)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libg16.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -40,6 +40,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_hgemm_use_packed_b": (_I, [_I, _I, _I, _I]),
     "g16_mm_t_scratch_bytes": (_SZ, [_I, _I, _I, _I]),
     "g16_mm_t_gemm": (_I, [_P, _I, _P, _P, _I, _P, _F, _I, _I, _I, _I, _P, _SZ, _P, _SZ, _P, _SZ, _P]),
+    "g16_mm_t_spec_history": (_I, [_P]),
     "g16_mm_t_spec_paused": (_I, [_P, _P]),
     "g16_packed_b_bytes": (_SZ, [_I, _I]),
     "g16_pack_weight": (_I, [_P, _P, _I, _I, _P]),

@@ -21,6 +21,8 @@ TARGET_ARCH = "gfx950"
 
 _cus: dict[int, int] = {}
 _arch_ok: dict[int, bool] = {}
+# Devices whose speculation history (g16_mm_t_spec_history) is enabled.
+_spec_history: set[int] = set()
 
 
 def _dev_index(device) -> int:
@@ -190,7 +192,14 @@ def mm_t(x2d: torch.Tensor, w_t: torch.Tensor, bias: torch.Tensor | None = None,
     # library call runs the rowscale cast into `scratch` and the GEMM on the planned route: the
     # tile-packed 256-row tiles for large outputs, split-K where the tiles leave CUs idle, else the
     # plain tiles (the cast, scales and GEMM of ops.py:86-108); on the unsplit 32x128 tile with
-    # K <= 1280 the GEMM casts its own rows into LDS, one launch in all.
+    # K <= 1280 the GEMM casts fp32 rows into LDS, and fp16 x on the 32-, 64- and 128-row tiles is
+    # streamed as it is (a row within the threshold is its own cast): one launch in both cases.
+    # The speculation history lets a weight whose fp16 call needed a tile computed again take the
+    # two-launch route for a while; it is enabled once per device (a small pinned allocation,
+    # retried on a later call if this one is being captured into a graph).
+    if x2d.dtype == torch.float16 and dev.index not in _spec_history:
+        if lib.g16_mm_t_spec_history(stream) == 0:
+            _spec_history.add(dev.index)
     kind, scratch_bytes, _ks, ws_bytes, cnt_bytes = _gemm_route(lib, M, N, K, dev)
     out = torch.empty(M, N, device=dev, dtype=out_dtype)
     # no scratch where the GEMM casts its own rows into LDS (one launch, the unsplit small tile)

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 13
+#define G16_ABI_VERSION 14
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -132,7 +132,8 @@ int g16_hgemm_use_packed(int M, int N, int K, int num_cus);
  *   only where some |x| of it exceeds the threshold or is NaN (split tiles: the last slice to
  *   arrive recomputes every slice). Same result bits; no scratch is used. A weight whose call had
  *   a tile computed again takes the other route below for its next 63 calls when the scratch the
- *   caller passed allows it (a per-device history in pinned host memory, keyed by w_t).
+ *   caller passed allows it (a per-device history in pinned host memory, keyed by w_t, once
+ *   g16_mm_t_spec_history has enabled it).
  *   One launch for fp32 x where the plan is the unsplit 32x128 tile and K <= 1280: the GEMM's
  *   workgroups cast their own rows of x into LDS (the rowscale arithmetic, the same bits) and no
  *   rowscale launch runs; g16_mm_t_scratch_bytes() is then 0 and scratch may be NULL (x must be
@@ -148,9 +149,17 @@ int g16_mm_t_gemm(const void* x, int x_is_f32, const uint16_t* w_t, void* out, i
                   const float* bias, float thresh, int M, int N, int K, int num_cus, void* scratch,
                   size_t scratch_bytes, void* workspace, size_t workspace_bytes, uint32_t* counters,
                   size_t counter_bytes, void* stream);
+/* Enables the speculation history for the device that owns `stream` (no counterpart in the
+ * reference): allocates 4 KB of pinned host memory once per device (kept until the process ends)
+ * into which the one-launch fp16 kernels report a recomputation. Until it is called,
+ * g16_mm_t_gemm keeps the one-launch route for every call. Returns 0, or the HIP error of the
+ * allocation (hipErrorStreamCaptureUnsupported while `stream` is being captured). Thread-safe;
+ * later calls return 0 at once. The GEMM entry points themselves never allocate. */
+int g16_mm_t_spec_history(void* stream);
 /* 1 if the speculation history of the device that owns `stream` routes g16_mm_t_gemm's next call
  * with this w_t around the one-launch fp16 route (a recent call with it was computed again), else
- * 0. For tests and diagnostics; no counterpart in the reference. */
+ * 0 (also when the history is not enabled). For tests and diagnostics; no counterpart in the
+ * reference. */
 int g16_mm_t_spec_paused(const uint16_t* w_t, void* stream);
 
 /* ---------------------------------------------------------------------------------------------

@@ -235,6 +235,8 @@ def test_a_recomputed_weight_takes_the_other_route_for_63_calls(lib, cus, cuda, 
     bufs = _bufs(lib, M, N, K, cus, cuda)
     ks, ws, wsb, cnt, cb = bufs
     stream = torch.cuda.current_stream(cuda).cuda_stream
+    assert lib.g16_mm_t_spec_history(stream) == 0   # enabled once per device (idempotent)
+    assert lib.g16_mm_t_spec_history(stream) == 0
     sb = lib.g16_mm_t_scratch_bytes(M, N, K, cus)
     assert (sb > 0) == with_scratch
     scratch = torch.empty(max(sb, 16), dtype=torch.uint8, device=cuda)
