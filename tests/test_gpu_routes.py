@@ -7,7 +7,9 @@ exactly as configured.
   deterministic, README.md:79; tests/test_correctness.py:52-59 checks repeatability).
 * Each split-K tile through ``mm_t``: the 128x128 tile split twice (512x4096x4096), the 64x128
   tile split twice (64x4096x11008), the 128x128 tile unsplit and split with an odd number of K
-  steps and a ragged last step, and the 32x128 tile of C3. The tile each case runs on is read from
+  steps and a ragged last step, and the 32x128 tile of C3. The packed-weight 256x256 and 256x128
+  tiles the planner falls back to when no 4-wavefront grid fits one round (M >= 512, long K, large
+  N) run unsplit. The tile each case runs on is read from
   the library's split-buffer sizes, so a plan change that moves a case to another tile fails here
   instead of silently dropping that tile from the tests.
 * The fp16-output golden fixtures (exact rational results, tests/golden/make_golden.py).
@@ -89,6 +91,8 @@ ROUTES = [
     (192, 4096, 512, (32, 128), 8),      # 32x128 split 8 ways at M > 64
     (768, 4056, 4096, (128, 128), 1),    # 128x128 unsplit: 127 K steps, the last one ragged
     (384, 4056, 3072, (128, 128), 3),    # split: slices of 44, 44 and 39 K steps, the last one ragged
+    (768, 4096, 11008, (256, 256), 1),   # no 4-wavefront grid fits one round: packed 256x256 tiles
+    (512, 4096, 11008, (256, 128), 1),   # ... packed 256x128 tiles where their grid fits one round
 ]
 
 
