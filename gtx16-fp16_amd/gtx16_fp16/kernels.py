@@ -7,6 +7,7 @@ enqueues on the stream it is given. Nothing is compiled at run time.
 """
 from __future__ import annotations
 
+import contextlib
 import threading
 
 import torch
@@ -28,16 +29,39 @@ KERNELS = {
 }
 
 
-def get_kernel(name: str, device: torch.device | None = None):
-    """The bound C entry point replacing reference kernel ``name`` (kernels.py:341-355). The
-    library holds code for every device it supports, so ``device`` only exists for signature
-    compatibility."""
-    del device
-    try:
-        sym = KERNELS[name]
-    except KeyError:
-        raise KeyError(f"unknown kernel {name!r}; known: {sorted(KERNELS)}") from None
-    return getattr(_clib.load(), sym)
+class Kernel:
+    """A reference kernel (kernels.py:139-250) bound to the library entry point that replaces it.
+    ``launch`` and ``PreparedLaunch`` take it with the reference's grid, block and argument list;
+    calling it directly calls the entry point with the C ABI's own arguments (``include/g16.h``)."""
+
+    __slots__ = ("name", "fn", "device_index")
+
+    def __init__(self, name: str, fn, device_index: int | None):
+        self.name = name
+        self.fn = fn
+        self.device_index = device_index
+
+    def __call__(self, *args):
+        return self.fn(*args)
+
+    def __repr__(self) -> str:
+        return f"Kernel({self.name!r} -> {KERNELS[self.name]}, device={self.device_index})"
+
+
+_kernels: dict[tuple[str, int | None], Kernel] = {}
+
+
+def get_kernel(name: str, device: torch.device | int | None = None) -> Kernel:
+    """The reference kernel ``name`` (kernels.py:341-355) on ``device``: the library holds code for
+    every device it supports, so nothing is compiled; the device only keys the split buffers of
+    the launches that need them (the current device at launch time when None)."""
+    if name not in KERNELS:
+        raise KeyError(f"unknown kernel {name!r}; known: {sorted(KERNELS)}")
+    idx = None if device is None else (torch.device(device).index or 0)
+    k = _kernels.get((name, idx))
+    if k is None:
+        k = _kernels[(name, idx)] = Kernel(name, getattr(_clib.load(), KERNELS[name]), idx)
+    return k
 
 
 def stream_handle(device_index: int) -> int:
@@ -51,15 +75,15 @@ def _arg(a):
     return a
 
 
-def launch(kernel, args: list, what: str = "g16 kernel") -> None:
+def call(fn, args: list, what: str = "g16 kernel") -> None:
     """Call a C entry point with tensors passed as device pointers and ``None`` as NULL; raise
-    ``RuntimeError`` on a nonzero status (kernels.py:299-321)."""
-    _clib.check(kernel(*[_arg(a) for a in args]), what)
+    ``RuntimeError`` on a nonzero status (kernels.py:299-302)."""
+    _clib.check(fn(*[_arg(a) for a in args]), what)
 
 
-class PreparedLaunch:
-    """A bound entry point whose per-call Python work is only the call itself: for the
-    token-by-token FastLinear path (kernels.py:324-338)."""
+class PreparedCall:
+    """A bound entry point whose per-call Python work is only the call itself, for the
+    token-by-token FastLinear path; raises ``RuntimeError`` on a nonzero status."""
 
     __slots__ = ("fn", "what")
 
@@ -71,6 +95,117 @@ class PreparedLaunch:
         status = self.fn(*args)
         if status != 0:
             _clib.check(status, self.what)
+
+
+# ---- the reference's launch interface (kernels.py:299-338) --------------------------------------
+# The reference launches its seven kernels with an explicit grid and block and the kernel's own
+# parameter list. Here each entry point plans its own launch shape, so grid and block are read
+# only for the sizes the reference passes through them (the rowscale kernel's row count, the
+# split count of the split-K and skinny kernels); the block is not used. Per kernel, the reference
+# arguments and what the call computes:
+#   rowscale_f32/_f16 [X, Y, S, K, thresh], grid (M, 1, 1): the same cast bits as the reference.
+#   hgemm_f32out/_f16out [A, B, C, bias, rscale, M, N, K]: C = rscale * (A @ B) + bias.
+#   hgemm_splitk [A, B, C, rscale, M, N, K, kchunk], grid z = slices: C += rscale * (A @ B), as the
+#     reference's fp32 atomics add into its prefilled C; the slices are summed in a fixed order
+#     into a temporary, which is then added to C (C must be a tensor).
+#   skinny_f32in/_f16in [A, B, C, bias, M, N, K, kchunk], grid y = slices: C = A @ B + bias. The
+#     reference adds into C and requires it zeroed (kernels.py:158); the result on a zeroed C is
+#     the same, and here C needs no zero-fill.
+_cus: dict[int, int] = {}
+
+
+def _num_cus(idx: int) -> int:
+    n = _cus.get(idx)
+    if n is None:
+        n = _cus[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return n
+
+
+def _device_index(kernel: Kernel, args) -> int:
+    if kernel.device_index is not None:
+        return kernel.device_index
+    for a in args:
+        if isinstance(a, torch.Tensor) and a.is_cuda:
+            return a.device.index or 0
+    return torch.cuda.current_device()
+
+
+def _slices(K: int, kchunk: int, grid_slices: int) -> int:
+    if K <= 0:
+        return 1
+    return max(1, -(-K // kchunk)) if kchunk > 0 else max(1, grid_slices)
+
+
+def _run(kernel: Kernel, grid, args: list, stream: int) -> None:
+    name, fn = kernel.name, kernel.fn
+    what = f"{name} ({KERNELS[name]})"
+    if name.startswith("rowscale"):
+        X, Y, S, K, thresh = args
+        _clib.check(fn(_arg(X), _arg(Y), _arg(S), int(grid[0]), int(K), float(thresh), stream), what)
+    elif name in ("hgemm_f32out", "hgemm_f16out"):
+        A, B, C, bias, rscale, M, N, K = args
+        _clib.check(fn(_arg(A), _arg(B), _arg(C), _arg(bias), _arg(rscale), int(M), int(N), int(K), stream), what)
+    elif name.startswith("skinny"):
+        A, B, C, bias, M, N, K, kchunk = args
+        M, N, K = int(M), int(N), int(K)
+        ks = _slices(K, int(kchunk), int(grid[1]))
+        lib = _clib.load()
+        dev = torch.device("cuda", _device_index(kernel, args))
+        ws = split_buffers(dev, stream, lib.g16_skinny_workspace_bytes(M, N, K, ks),
+                           lib.g16_skinny_counter_bytes(M, N, K, ks))
+        _clib.check(fn(_arg(A), _arg(B), _arg(C), _arg(bias), M, N, K, ks, *ws, stream), what)
+    elif name == "hgemm_splitk":
+        A, B, C, rscale, M, N, K, kchunk = args
+        if not isinstance(C, torch.Tensor) or C.dtype != torch.float32:
+            raise TypeError("hgemm_splitk adds into C: pass C as an fp32 tensor (through launch())")
+        M, N, K = int(M), int(N), int(K)
+        ks = _slices(K, int(kchunk), int(grid[2]))
+        lib = _clib.load()
+        idx = _device_index(kernel, args)
+        dev = torch.device("cuda", idx)
+        cus = _num_cus(idx)
+        ws = split_buffers(dev, stream, lib.g16_hgemm_splitk_workspace_bytes(M, N, K, ks, cus),
+                           lib.g16_hgemm_splitk_counter_bytes(M, N, K, ks, cus))
+        # the temporary and the addition run on the launch's stream, after the GEMM
+        on = (contextlib.nullcontext() if stream == stream_handle(idx)
+              else torch.cuda.stream(torch.cuda.ExternalStream(stream, device=dev)))
+        with on:
+            tmp = torch.empty(M, N, device=dev, dtype=torch.float32)
+            _clib.check(fn(_arg(A), _arg(B), tmp.data_ptr(), 0, None, _arg(rscale), M, N, K, ks, cus, *ws, stream),
+                        what)
+            C.view(M, N).add_(tmp)
+    else:  # pragma: no cover - KERNELS and this dispatch list the same seven names
+        raise KeyError(name)
+
+
+def launch(kernel: Kernel, grid: tuple[int, int, int], block: tuple[int, int, int], args: list, stream: int) -> None:
+    """The reference's launch (kernels.py:315-321): ``kernel`` from ``get_kernel``, its grid and
+    block, its argument list (tensors, None for NULL, ints, floats) and a raw stream handle
+    (``stream_handle``). Raises ``RuntimeError`` when the entry point returns a nonzero status."""
+    del block
+    _run(kernel, grid, list(args), stream)
+
+
+class PreparedLaunch:
+    """The reference's prepared launch (kernels.py:324-338): built once with the kernel, grid,
+    block and one character per argument ('p' pointer, 'i' int32, 'f' float32); each call passes
+    the stream handle and the argument values (pointers as ints or None)."""
+
+    __slots__ = ("kernel", "grid", "block", "kinds")
+
+    def __init__(self, kernel: Kernel, grid, block, kinds: str):
+        if len(kinds) != _ARITY[kernel.name] or set(kinds) - {"p", "i", "f"}:
+            raise ValueError(f"{kernel.name} takes {_ARITY[kernel.name]} arguments, kinds {kinds!r}")
+        if kernel.name == "hgemm_splitk":
+            raise TypeError("hgemm_splitk adds into C: launch it through launch() with C as a tensor")
+        self.kernel, self.grid, self.block, self.kinds = kernel, grid, block, kinds
+
+    def __call__(self, stream: int, *args) -> None:
+        _run(self.kernel, self.grid, list(args), stream)
+
+
+_ARITY = {"rowscale_f32": 5, "rowscale_f16": 5, "hgemm_f32out": 8, "hgemm_f16out": 8, "hgemm_splitk": 8,
+          "skinny_f32in": 8, "skinny_f16in": 8}
 
 
 # ---- split-reduction buffers ----------------------------------------------------------------

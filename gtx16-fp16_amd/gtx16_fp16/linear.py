@@ -9,7 +9,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _clib
-from .kernels import SKINNY_MAX_M, PreparedLaunch, split_buffers, stream_handle
+from .kernels import SKINNY_MAX_M, PreparedCall, split_buffers, stream_handle
 from .ops import _is_target, _sm_count, is_affected, mm_t, mm_t_prepacked, pack_weight, prepacked_route, supported
 
 
@@ -45,7 +45,7 @@ class FastLinear(nn.Module):
     def __init__(self, in_features: int, out_features: int, bias: bool = True, device=None):
         super().__init__()
         self.in_features, self.out_features = in_features, out_features
-        # (M, device index) -> (PreparedLaunch or None, ksplit, (partial, counter) bytes, weight pointer,
+        # (M, device index) -> (PreparedCall or None, ksplit, (partial, counter) bytes, weight pointer,
         # bias pointer) for the token-by-token fast path; None in the first field when the weight or
         # bias the pointers name cannot be handed to the kernel (the call then takes the general path).
         self._skinny: dict = {}
@@ -89,7 +89,7 @@ class FastLinear(nn.Module):
             if ok:
                 lib = _clib.load()
                 ksplit = lib.g16_skinny_plan(M, N, K, _sm_count(dev))
-                pl = PreparedLaunch(_clib.fast().skinny_f32in, "skinny GEMM")
+                pl = PreparedCall(_clib.fast().skinny_f32in, "skinny GEMM")
                 sizes = (lib.g16_skinny_workspace_bytes(M, N, K, ksplit), lib.g16_skinny_counter_bytes(M, N, K, ksplit))
             entry = (pl, ksplit, sizes, w.data_ptr(), bptr)
             self._skinny[key] = entry

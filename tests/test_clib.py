@@ -193,10 +193,65 @@ def test_fast_extension_matches_the_c_entry_points(lib):
 def test_nonzero_status_raises_runtime_error():
     # kernels.py:299-302 convention: a failed launch raises RuntimeError naming the status
     with pytest.raises(RuntimeError, match="status 98"):
-        kernels.launch(lambda *a: 98, [1, 2], "fake kernel")
+        kernels.call(lambda *a: 98, [1, 2], "fake kernel")
     with pytest.raises(RuntimeError, match="skinny"):
-        kernels.PreparedLaunch(lambda *a: -4, "skinny GEMM")(1, 2)
-    kernels.PreparedLaunch(lambda *a: 0, "ok")()
+        kernels.PreparedCall(lambda *a: -4, "skinny GEMM")(1, 2)
+    kernels.PreparedCall(lambda *a: 0, "ok")()
+
+
+def test_launch_interface_has_the_reference_signatures():
+    # kernels.py:315 launch(kernel, grid, block, args, stream); kernels.py:327-336
+    # PreparedLaunch(kernel, grid, block, kinds) called as (stream, *args)
+    import inspect
+
+    assert list(inspect.signature(kernels.launch).parameters) == ["kernel", "grid", "block", "args", "stream"]
+    assert list(inspect.signature(kernels.PreparedLaunch).parameters) == ["kernel", "grid", "block", "kinds"]
+    assert list(inspect.signature(kernels.PreparedLaunch.__call__).parameters) == ["self", "stream", "args"]
+    assert list(inspect.signature(kernels.get_kernel).parameters) == ["name", "device"]
+
+
+def _recording(name, status=0):
+    """A kernel of the reference's name whose entry point records its C arguments."""
+    seen = []
+
+    def fn(*a):
+        seen.append(a)
+        return status
+
+    return kernels.Kernel(name, fn, 0), seen
+
+
+def test_launch_maps_reference_arguments_to_the_entry_points():
+    # the argument lists ops.py builds (ops.py:89-90, 106-108) reach the C entry points in their
+    # order (include/g16.h), with the row count taken from the rowscale grid
+    k, seen = _recording("rowscale_f32")
+    kernels.launch(k, (48, 1, 1), (256, 1, 1), [0x1000, 0x2000, 0x3000, 64, 1024.0], 7)
+    assert seen == [(0x1000, 0x2000, 0x3000, 48, 64, 1024.0, 7)]
+    k, seen = _recording("hgemm_f16out")
+    kernels.launch(k, (2, 3, 1), (256, 1, 1), [0x10, 0x20, 0x30, None, 0x40, 300, 256, 64], 9)
+    assert seen == [(0x10, 0x20, 0x30, None, 0x40, 300, 256, 64, 9)]
+    k, seen = _recording("hgemm_f32out", status=4)
+    with pytest.raises(RuntimeError, match="hgemm_f32out"):
+        kernels.launch(k, (1, 1, 1), (256, 1, 1), [0x10, 0x20, 0x30, None, None, 8, 8, 8], 0)
+
+
+def test_prepared_launch_checks_its_kinds_and_refuses_accumulating_split_k():
+    k, seen = _recording("rowscale_f16")
+    pl = kernels.PreparedLaunch(k, (4, 1, 1), (256, 1, 1), "pppif")
+    pl(5, 0x100, 0x200, 0x300, 16, 1024.0)
+    assert seen == [(0x100, 0x200, 0x300, 4, 16, 1024.0, 5)]
+    with pytest.raises(ValueError):
+        kernels.PreparedLaunch(k, (4, 1, 1), (256, 1, 1), "ppp")
+    with pytest.raises(TypeError, match="adds into C"):
+        kernels.PreparedLaunch(kernels.Kernel("hgemm_splitk", None, 0), (1, 1, 2), (256, 1, 1), "ppppiiii")
+
+
+def test_split_counts_follow_the_reference_kchunk():
+    # ops.py:48-50, 95-97: slices = ceil(K / kchunk); the grid's slice count when kchunk is 0
+    assert kernels._slices(4096, 512, 99) == 8
+    assert kernels._slices(4100, 520, 99) == 8
+    assert kernels._slices(64, 0, 3) == 3
+    assert kernels._slices(0, 0, 5) == 1
 
 
 def test_missing_library_fails_loudly(tmp_path):
@@ -207,6 +262,7 @@ def test_missing_library_fails_loudly(tmp_path):
 def test_get_kernel_names_match_reference_kernels():
     assert set(kernels.KERNELS) == {"rowscale_f32", "rowscale_f16", "hgemm_f32out", "hgemm_f16out",
                                     "hgemm_splitk", "skinny_f32in", "skinny_f16in"}
-    assert kernels.get_kernel("hgemm_f32out") is not None
+    k = kernels.get_kernel("hgemm_f32out")
+    assert k.name == "hgemm_f32out" and k.fn is not None and kernels.get_kernel("hgemm_f32out") is k
     with pytest.raises(KeyError):
         kernels.get_kernel("hgemm")
