@@ -32,9 +32,10 @@
 //     barrier); the 4-wavefront tiles interleave DMA, MFMAs and the next step's fragment reads
 //     (fragments double-buffered in registers) with one barrier per step.
 //   * Tiles are assigned XCD-aware: the hardware deals workgroups round-robin over the 8 XCDs, so
-//     workgroup b is mapped to tile (b % 8) * (T / 8) + b / 8, giving each XCD a contiguous run
-//     of tiles, which a grouped (GROUP_M rows at a time) order turns into a compact 2-D block
-//     that shares A rows and B columns in that XCD's L2.
+//     workgroup b is mapped to tile (b % 8) * (T / 8) + b / 8 when the T tiles are a multiple of 8
+//     (and, for unsplit grids of any other count, to the same contiguous runs of T / 8 or T / 8 + 1
+//     tiles per XCD), giving each XCD a contiguous run of tiles, which a grouped (GROUP_M rows at a
+//     time) order turns into a compact 2-D block that shares A rows and B columns in that XCD's L2.
 //   * Resident A (the unsplit 32x128 tile with K <= kResidentSteps * 64, mm_t's GEMM path in one
 //     launch): the workgroup reads its 32 rows of the fp32/fp16 activations itself, computes each
 //     row's scale (rowscale_math.hpp, the rowscale kernel's arithmetic) and writes the scaled fp16
@@ -44,10 +45,11 @@
 //     launch): a row whose |max| does not exceed the threshold has scale 1, and its rowscale cast is
 //     the activation itself. So the GEMM streams x as A and tracks the largest |x| it multiplies
 //     (from the A fragments). If no row of the tile exceeds the threshold, the result is the cast
-//     path's, bit for bit. Otherwise the tile is computed again from the rescaled cast: unsplit
-//     tiles right away (cast into LDS for the resident tile, else into the scratch buffer), split
-//     tiles by the slice that arrives last (every flagged slice marks the arrival count), which
-//     recomputes every slice in slice order -- the same sums the split reduction adds.
+//     path's, bit for bit. Otherwise the tile is computed again with its A fragments multiplied in
+//     registers by the rows' factors 2^-e (an exact product rounded once, with fp16 denormals kept:
+//     the rowscale cast's value): unsplit tiles right away, split tiles by the slice that arrives
+//     last (every flagged slice marks the arrival count), which recomputes every slice in slice
+//     order -- the same sums the split reduction adds.
 //   * Split-K: slice z of tile t covers K range [z*kchunk, (z+1)*kchunk). Every slice stores its
 //     fp32 accumulators to the workspace in the lanes' own register order (fully coalesced 16-byte
 //     device-coherent stores); the last slice to arrive adds all slices in slice order and runs the

@@ -249,6 +249,37 @@ def test_graphs_of_mm_t_keep_their_buffers_when_a_later_capture_outgrows_them(g,
             assert torch.equal(o, e)
 
 
+@pytest.mark.parametrize("shapes", [
+    ((64, 4096, 1024, torch.float16), (64, 4096, 1024, torch.float16)),  # one split-K route on both
+    ((64, 4096, 1024, torch.float32), (4, 4096, 4096, torch.float32)),  # split-K cast + GEMM; skinny
+])
+def test_concurrent_streams_keep_their_own_split_buffers(g, cuda, shapes):
+    # Calls on different streams may run at the same time, so each stream has its own split
+    # partials, counters and cast scratch: interleaved launches on two streams give the serial
+    # results bit for bit.
+    ins = []
+    for i, (M, K, N, dt) in enumerate(shapes):
+        gen = torch.Generator(cuda).manual_seed(300 + i)
+        x = torch.randn(M, K, device=cuda, generator=gen).to(dt)
+        w = (torch.randn(K, N, device=cuda, generator=gen) * 0.02).half()
+        b = torch.randn(N, device=cuda, generator=gen) * 0.02
+        ins.append((x, w, b))
+    ref = [g.mm_t(x, w, b) for x, w, b in ins]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(cuda) for _ in ins]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(cuda))
+    outs = [[] for _ in ins]
+    for _ in range(25):
+        for s, (x, w, b), o in zip(streams, ins, outs):
+            with torch.cuda.stream(s):
+                o.append(g.mm_t(x, w, b))
+    torch.cuda.synchronize()
+    for r, o in zip(ref, outs):
+        for k, y in enumerate(o):
+            assert torch.equal(y, r), k
+
+
 def test_gemm_clock_stamps_give_a_plausible_clock(cuda):
     # g16_gemm_clock: workgroup 0's main-loop shader cycles and 100 MHz ticks of the latest GEMM
     from gtx16_fp16 import _clib
