@@ -257,729 +257,740 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // columns: ranges of ntiles / 8 tiles; with an unsplit grid of another size, ranges of
   // floor(ntiles / 8) or one more. (For split grids of such sizes the linear order is kept: a
   // slice-major mapping measured 1-3 us slower there.)
+  // A grid of fewer workgroups than tiles (the unsplit 256-row tiles past one round: one workgroup
+  // per CU, a multiple of 8) is persistent: workgroup b computes tiles b, b + gridDim.x, ... in
+  // turn, so each XCD still walks its own contiguous range, and a tile's epilogue stores drain
+  // while the next tile's DMA and MFMAs start (65536 x 768 x 768 on 256 CUs: 101.9 -> 94.4 us;
+  // 65536 x 768 x 3072: 371 -> 357 us), instead of each round's workgroups retiring and new ones
+  // being dispatched. A split grid always has one workgroup per tile, so its early returns below
+  // end the workgroup's only tile.
   const int ntiles = ntm * ntn;
-  int lin = blockIdx.x;
-  if (ntiles % 8 == 0) {
-    lin = (lin % 8) * (ntiles / 8) + lin / 8;
-  } else if (gridDim.y == 1) {
-    const int xcd = lin % 8, q8 = ntiles / 8, r8 = ntiles % 8;
-    lin = xcd * q8 + min(xcd, r8) + lin / 8;  // XCD x holds q8 + (x < r8) workgroups
-  }
-  const int per_group = kGroupM * ntn;
-  const int first_m = (lin / per_group) * kGroupM;
-  const int gsz = min(ntm - first_m, kGroupM);
-  const int tm = first_m + (lin % per_group) % gsz;
-  const int tn = (lin % per_group) / gsz;
-  const int tile = tm * ntn + tn;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int z = blockIdx.y;
-  // this slice's K range (the speculative path's recomputation walks every slice's range)
-  int kbeg = z * kchunk;
-  int kend = min(K, kbeg + kchunk);
-  int nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool stamps = blockIdx.x == 0 && blockIdx.y == 0;  // workgroup 0 records the loop's clock
-  unsigned long long clk_c0 = 0, clk_r0 = 0;
-  if (stamps) {
-    clk_c0 = __builtin_amdgcn_s_memtime();
-    clk_r0 = __builtin_amdgcn_s_memrealtime();
-  }
-  const int wm0 = (wave / Cfg::WGN) * Cfg::WTM;
-  const int wn0 = (wave % Cfg::WGN) * Cfg::WTN;
-
-  // ---- DMA staging: per-lane chunk assignment (independent of k) ----
-  const int a_row0 = wave * Cfg::A_INSTR * Cfg::A_ROWS_PER_INSTR + lane / Cfg::A_ROW_CHUNKS;
-  const int a_phys = lane % Cfg::A_ROW_CHUNKS;
-  const int b_row0 = wave * Cfg::B_INSTR * Cfg::B_ROWS_PER_INSTR + lane / Cfg::B_ROW_CHUNKS;
-  const int b_phys = lane % Cfg::B_ROW_CHUNKS;
-
-  // DMA of K step k0 into stage `st`, one 1 KB instruction at a time (instruction d < A_INSTR: A,
-  // else B). Steps past the slice are all out of range (zeros, no traffic): they keep the number
-  // of DMA operations per step constant, which the vmcnt waits rely on.
-  auto rsrc_a = [&](int k0) {
-    if constexpr (PACKED_A) {
-      static_assert(Cfg::BM == 256 && Cfg::BK == 32 && !SPLITK, "packed A is the stage image of 256 rows x 32 K");
-      return __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<_Float16*>(A) + static_cast<size_t>(tm) * ceil_div(K, BK) * (Cfg::A_BYTES / 2), 0, 0x7fffffff,
-          kRawBufferDword3);
-    } else {
-      return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A) + static_cast<size_t>(m0) * K + k0, 0,
-                                               0x7fffffff, kRawBufferDword3);
+  for (int work = blockIdx.x; work < ntiles; work += gridDim.x) {
+    int lin = work;
+    if (ntiles % 8 == 0) {
+      lin = (lin % 8) * (ntiles / 8) + lin / 8;
+    } else if (gridDim.y == 1) {
+      const int xcd = lin % 8, q8 = ntiles / 8, r8 = ntiles % 8;
+      lin = xcd * q8 + min(xcd, r8) + lin / 8;  // XCD x holds q8 + (x < r8) workgroups
     }
-  };
-  auto rsrc_b = [&](int k0) {
-    if constexpr (PACKED_B) {
-      // The packed weight holds B^T in 256-row blocks (g16_pack_weight). A 256-column tile streams
-      // whole 16 KB blocks; a 128-column tile streams one half of each: rows 0-127 of a block are
-      // its first 8 KB (chunks q < 8), rows 128-255 the second, each already the 128-row stage
-      // image (the row swizzle repeats every 8 rows). Step k0 adds k0/BK blocks (16 KB) either way.
-      static_assert(PACKED_A && (Cfg::BN == 256 || Cfg::BN == 128), "packed weight: the 256-row tiles");
-      constexpr int kHalves = 256 / Cfg::BN;
-      return __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<_Float16*>(B) + static_cast<size_t>(tn / kHalves) * ceil_div(K, BK) * 8192 + (tn % kHalves) * 4096, 0,
-          0x7fffffff, kRawBufferDword3);
-    } else {
-      return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B) + static_cast<size_t>(k0) * N + n0, 0,
-                                               0x7fffffff, kRawBufferDword3);
-    }
-  };
-  auto dma_op = [&](int st, int k0, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int d) {
-    if (d < Cfg::A_INSTR && PACKED_A) {
-      // Tile-packed A (g16_rowscale_pack_*): the stage image of step k0 is one contiguous 16 KB
-      // block; instruction q of the stage copies its q-th KB. ra is based at this tile row.
-      const int q = wave * Cfg::A_INSTR + d;
-      // uniform part of the offset (kOob for a step past the slice) plus this lane's 16 bytes;
-      // the sum of kOob and a lane part (< 16 KB) is still past the descriptor's range: zeros
-      const uint32_t step_off = k0 < kend ? static_cast<uint32_t>(k0) / BK * 16384u : kOob;
-      dma16(ra, sA_lds + st * Cfg::A_BYTES + q * 1024, step_off + (q * 64 + lane) * 16);
-    } else if (d < Cfg::A_INSTR) {
-      const int row = a_row0 + d * Cfg::A_ROWS_PER_INSTR;
-      const int c = a_phys ^ Cfg::swz_a(row);
-      const bool ok = (m0 + row < M) && (k0 + c * 8 < kend);
-      const uint32_t off = ok ? static_cast<uint32_t>((row * K + c * 8) * 2) : kOob;
-      dma16(ra, sA_lds + st * Cfg::A_BYTES + (wave * Cfg::A_INSTR + d) * 1024, off);
-    } else if (PACKED_B) {
-      // Packed weight (g16_pack_weight): B^T's stage image, like packed A.
-      const int q = wave * Cfg::B_INSTR + (d - Cfg::A_INSTR);
-      const uint32_t step_off = k0 < kend ? static_cast<uint32_t>(k0) / BK * 16384u : kOob;
-      dma16(rb, sB_lds + st * Cfg::B_BYTES + q * 1024, step_off + (q * 64 + lane) * 16);
-    } else {
-      const int i = d - Cfg::A_INSTR;
-      const int row = b_row0 + i * Cfg::B_ROWS_PER_INSTR;
-      const int c = b_phys ^ Cfg::swz_b(row);
-      const bool ok = (k0 + row < kend) && (n0 + c * 8 < N);
-      const uint32_t off = ok ? static_cast<uint32_t>((row * N + c * 8) * 2) : kOob;
-      dma16(rb, sB_lds + st * Cfg::B_BYTES + (wave * Cfg::B_INSTR + i) * 1024, off);
-    }
-  };
-  auto dma = [&](int st, int k0) {
-    const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
-#pragma unroll
-    for (int d = 0; d < Cfg::DMA_PER_STEP; ++d) dma_op(st, k0, ra, rb, d);
-  };
-  // Inside the K loops, B's descriptor for successive steps comes from a running pointer (row-major
-  // B: one 64-bit add per step instead of a 64-bit multiply); b_run is set to the first step's base
-  // before each loop, and every call advances it by one step.
-  const _Float16* b_run = nullptr;
-  auto rsrc_b_next = [&](int k0) {
-    if constexpr (PACKED_B) {
-      return rsrc_b(k0);
-    } else {
-      const __amdgpu_buffer_rsrc_t r =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(b_run), 0, 0x7fffffff, kRawBufferDword3);
-      b_run += static_cast<size_t>(BK) * N;
-      return r;
-    }
-  };
+    const int per_group = kGroupM * ntn;
+    const int first_m = (lin / per_group) * kGroupM;
+    const int gsz = min(ntm - first_m, kGroupM);
+    const int tm = first_m + (lin % per_group) % gsz;
+    const int tn = (lin % per_group) / gsz;
+    const int tile = tm * ntn + tn;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int z = blockIdx.y;
+    // this slice's K range (the speculative path's recomputation walks every slice's range)
+    int kbeg = z * kchunk;
+    int kend = min(K, kbeg + kchunk);
+    int nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
 
-  // ---- fragment addressing (byte offsets within a stage) ----
-  // MFMA operands (both shapes): lane l holds the 8-deep k-run 8*(l/MB) .. +7 of the MFMA's K step
-  // for A row l%MB (B column l%MB). A and B use the same lane -> k assignment, so the product does
-  // not depend on how the instruction orders k internally.
-  const int frow = lane & (MB - 1);  // A fragment row (B^T row) within a block
-  const int fk = lane / MB;          // which 8-run of the MK-deep K step
-  // B transposed reads: the 16-lane group g covers columns +16*(g&1) and k rows +8*(g>>1) of a
-  // 32x16 step (32x32x16), or k rows +8*g of a 16x32 step (16x16x32); lane q of the group
-  // addresses row q/4, columns 4*(q%4).
-  const int bg = lane >> 4, bq = lane & 15;
-  const int b_col_in = (Cfg::MF16 ? 0 : 16 * (bg & 1)) + 4 * (bq & 3);  // column within the block
-  const int b_k_in = 8 * (Cfg::MF16 ? bg : (bg >> 1)) + (bq >> 2);      // k row within the step (first read)
-
-  auto a_off = [&](int i, int ks) {
-    const int row = wm0 + MB * i + frow;
-    const int chunk = ks * (MK / 8) + fk;
-    return row * (BK * 2) + ((chunk ^ Cfg::swz_a(row)) * 16);
-  };
-  auto b_off = [&](int j, int krow) {
-    const int col = wn0 + MB * j + b_col_in;
-    return krow * (BN * 2) + (((col >> 3) ^ Cfg::swz_b(krow)) * 16) + (col & 7) * 2;
-  };
-  // Every k row one lane reads in a step (b_k_in, +4, +MK per substep) has the same swizzle (see
-  // swz_b): b_off(j, b_k_in + r) = b_off(j, b_k_in) + r * BN * 2. One LDS address per block, offset
-  // by the stage base, serves all of a step's transposing reads.
-  uint32_t b_tr[TN];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) b_tr[j] = sB_lds + static_cast<uint32_t>(b_off(j, b_k_in));
-
-  using AccT = std::conditional_t<Cfg::MF16, float4v, float16v>;
-  AccT acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
-
-  // Fragments of one whole K step (BK/MK MFMA substeps), double-buffered across steps: the MFMAs
-  // of step j run on set j&1 while the LDS reads of step j+1 fill set (j+1)&1.
-  constexpr int KS = BK / MK;
-  half8 af[2][KS][TM], bf[2][KS][TN];
-  // Speculative A: the largest and smallest x this lane has multiplied, per fragment row i and per
-  // fp16 half of a dword (lane l's A fragments i are all of row wm0 + 32 i + l % 32). The IEEE
-  // maximum/minimum propagate a NaN, so a NaN counts as above the threshold, which only costs a
-  // recompute. Chains of two become v_pk_maximum3_f16 / v_pk_minimum3_f16: 4 VALU instructions per
-  // 8-value fragment.
-  half2v xmax[TM] = {}, xmin[TM] = {};
-  auto track_amax = [&](int buf) {
-    if constexpr (SPEC) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const half8 v = af[buf][ks][i];
-          const half2v d0 = __builtin_shufflevector(v, v, 0, 1), d1 = __builtin_shufflevector(v, v, 2, 3);
-          const half2v d2 = __builtin_shufflevector(v, v, 4, 5), d3 = __builtin_shufflevector(v, v, 6, 7);
-          xmax[i] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(xmax[i], d0), d1);
-          xmax[i] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(xmax[i], d2), d3);
-          xmin[i] = __builtin_elementwise_minimum(__builtin_elementwise_minimum(xmin[i], d0), d1);
-          xmin[i] = __builtin_elementwise_minimum(__builtin_elementwise_minimum(xmin[i], d2), d3);
-        }
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool stamps = blockIdx.x == 0 && blockIdx.y == 0;  // workgroup 0 records the loop's clock
+    unsigned long long clk_c0 = 0, clk_r0 = 0;
+    if (stamps) {
+      clk_c0 = __builtin_amdgcn_s_memtime();
+      clk_r0 = __builtin_amdgcn_s_memrealtime();
     }
-  };
-  // The recomputation's cast: fp16_rne(x * 2^-e) of each fragment row, as one fp16 multiply by the
-  // row's factor 2^-e (0 for a row whose scale is +inf): the product is exact before rounding, and
-  // fp16 denormals are kept, so it is the rowscale cast's value bit for bit (e <= 24 here).
-  half2v fac[TM];
-  auto scale_frags = [&](int buf) {
-    if constexpr (SPEC) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-          af[buf][ks][i] *= __builtin_shufflevector(fac[i], fac[i], 0, 1, 0, 1, 0, 1, 0, 1);
-    }
-  };
-  // fragment read f of a step: f = ks * (TM + TN) + (i < TM ? i : TM + j)
-  // st: the ring stage of B (and of A); sta: A's stage where it differs (the resident-A tile keeps
-  // every K step's A image in its own stage)
-  auto frag_op = [&](int buf, int st, int f, int sta = -1) {
-    const int ks = f / (TM + TN), w = f % (TM + TN);
-    if (w < TM) {
-      af[buf][ks][w] = *reinterpret_cast<const half8*>(&sA[sta < 0 ? st : sta][a_off(w, ks)]);
-    } else if constexpr (PACKED_B) {
-      // B^T stored [n][k] like A: one 16-byte read gives lane l the k-run of column l%32.
-      const int j = w - TM;
-      const int row = wn0 + MB * j + frow;
+    const int wm0 = (wave / Cfg::WGN) * Cfg::WTM;
+    const int wn0 = (wave % Cfg::WGN) * Cfg::WTN;
+
+    // ---- DMA staging: per-lane chunk assignment (independent of k) ----
+    const int a_row0 = wave * Cfg::A_INSTR * Cfg::A_ROWS_PER_INSTR + lane / Cfg::A_ROW_CHUNKS;
+    const int a_phys = lane % Cfg::A_ROW_CHUNKS;
+    const int b_row0 = wave * Cfg::B_INSTR * Cfg::B_ROWS_PER_INSTR + lane / Cfg::B_ROW_CHUNKS;
+    const int b_phys = lane % Cfg::B_ROW_CHUNKS;
+
+    // DMA of K step k0 into stage `st`, one 1 KB instruction at a time (instruction d < A_INSTR: A,
+    // else B). Steps past the slice are all out of range (zeros, no traffic): they keep the number
+    // of DMA operations per step constant, which the vmcnt waits rely on.
+    auto rsrc_a = [&](int k0) {
+      if constexpr (PACKED_A) {
+        static_assert(Cfg::BM == 256 && Cfg::BK == 32 && !SPLITK, "packed A is the stage image of 256 rows x 32 K");
+        return __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>(A) + static_cast<size_t>(tm) * ceil_div(K, BK) * (Cfg::A_BYTES / 2), 0, 0x7fffffff,
+            kRawBufferDword3);
+      } else {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A) + static_cast<size_t>(m0) * K + k0, 0,
+                                                 0x7fffffff, kRawBufferDword3);
+      }
+    };
+    auto rsrc_b = [&](int k0) {
+      if constexpr (PACKED_B) {
+        // The packed weight holds B^T in 256-row blocks (g16_pack_weight). A 256-column tile streams
+        // whole 16 KB blocks; a 128-column tile streams one half of each: rows 0-127 of a block are
+        // its first 8 KB (chunks q < 8), rows 128-255 the second, each already the 128-row stage
+        // image (the row swizzle repeats every 8 rows). Step k0 adds k0/BK blocks (16 KB) either way.
+        static_assert(PACKED_A && (Cfg::BN == 256 || Cfg::BN == 128), "packed weight: the 256-row tiles");
+        constexpr int kHalves = 256 / Cfg::BN;
+        return __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>(B) + static_cast<size_t>(tn / kHalves) * ceil_div(K, BK) * 8192 + (tn % kHalves) * 4096, 0,
+            0x7fffffff, kRawBufferDword3);
+      } else {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B) + static_cast<size_t>(k0) * N + n0, 0,
+                                                 0x7fffffff, kRawBufferDword3);
+      }
+    };
+    auto dma_op = [&](int st, int k0, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int d) {
+      if (d < Cfg::A_INSTR && PACKED_A) {
+        // Tile-packed A (g16_rowscale_pack_*): the stage image of step k0 is one contiguous 16 KB
+        // block; instruction q of the stage copies its q-th KB. ra is based at this tile row.
+        const int q = wave * Cfg::A_INSTR + d;
+        // uniform part of the offset (kOob for a step past the slice) plus this lane's 16 bytes;
+        // the sum of kOob and a lane part (< 16 KB) is still past the descriptor's range: zeros
+        const uint32_t step_off = k0 < kend ? static_cast<uint32_t>(k0) / BK * 16384u : kOob;
+        dma16(ra, sA_lds + st * Cfg::A_BYTES + q * 1024, step_off + (q * 64 + lane) * 16);
+      } else if (d < Cfg::A_INSTR) {
+        const int row = a_row0 + d * Cfg::A_ROWS_PER_INSTR;
+        const int c = a_phys ^ Cfg::swz_a(row);
+        const bool ok = (m0 + row < M) && (k0 + c * 8 < kend);
+        const uint32_t off = ok ? static_cast<uint32_t>((row * K + c * 8) * 2) : kOob;
+        dma16(ra, sA_lds + st * Cfg::A_BYTES + (wave * Cfg::A_INSTR + d) * 1024, off);
+      } else if (PACKED_B) {
+        // Packed weight (g16_pack_weight): B^T's stage image, like packed A.
+        const int q = wave * Cfg::B_INSTR + (d - Cfg::A_INSTR);
+        const uint32_t step_off = k0 < kend ? static_cast<uint32_t>(k0) / BK * 16384u : kOob;
+        dma16(rb, sB_lds + st * Cfg::B_BYTES + q * 1024, step_off + (q * 64 + lane) * 16);
+      } else {
+        const int i = d - Cfg::A_INSTR;
+        const int row = b_row0 + i * Cfg::B_ROWS_PER_INSTR;
+        const int c = b_phys ^ Cfg::swz_b(row);
+        const bool ok = (k0 + row < kend) && (n0 + c * 8 < N);
+        const uint32_t off = ok ? static_cast<uint32_t>((row * N + c * 8) * 2) : kOob;
+        dma16(rb, sB_lds + st * Cfg::B_BYTES + (wave * Cfg::B_INSTR + i) * 1024, off);
+      }
+    };
+    auto dma = [&](int st, int k0) {
+      const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
+  #pragma unroll
+      for (int d = 0; d < Cfg::DMA_PER_STEP; ++d) dma_op(st, k0, ra, rb, d);
+    };
+    // Inside the K loops, B's descriptor for successive steps comes from a running pointer (row-major
+    // B: one 64-bit add per step instead of a 64-bit multiply); b_run is set to the first step's base
+    // before each loop, and every call advances it by one step.
+    const _Float16* b_run = nullptr;
+    auto rsrc_b_next = [&](int k0) {
+      if constexpr (PACKED_B) {
+        return rsrc_b(k0);
+      } else {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(b_run), 0, 0x7fffffff, kRawBufferDword3);
+        b_run += static_cast<size_t>(BK) * N;
+        return r;
+      }
+    };
+
+    // ---- fragment addressing (byte offsets within a stage) ----
+    // MFMA operands (both shapes): lane l holds the 8-deep k-run 8*(l/MB) .. +7 of the MFMA's K step
+    // for A row l%MB (B column l%MB). A and B use the same lane -> k assignment, so the product does
+    // not depend on how the instruction orders k internally.
+    const int frow = lane & (MB - 1);  // A fragment row (B^T row) within a block
+    const int fk = lane / MB;          // which 8-run of the MK-deep K step
+    // B transposed reads: the 16-lane group g covers columns +16*(g&1) and k rows +8*(g>>1) of a
+    // 32x16 step (32x32x16), or k rows +8*g of a 16x32 step (16x16x32); lane q of the group
+    // addresses row q/4, columns 4*(q%4).
+    const int bg = lane >> 4, bq = lane & 15;
+    const int b_col_in = (Cfg::MF16 ? 0 : 16 * (bg & 1)) + 4 * (bq & 3);  // column within the block
+    const int b_k_in = 8 * (Cfg::MF16 ? bg : (bg >> 1)) + (bq >> 2);      // k row within the step (first read)
+
+    auto a_off = [&](int i, int ks) {
+      const int row = wm0 + MB * i + frow;
       const int chunk = ks * (MK / 8) + fk;
-      bf[buf][ks][j] = *reinterpret_cast<const half8*>(
-          &sB[st][row * (BK * 2) + ((chunk ^ Cfg::swz_a(row)) * 16)]);
-    } else {
-      const int j = w - TM;
-      const uint32_t at = b_tr[j] + st * Cfg::B_BYTES + ks * MK * (BN * 2);
-      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds4_at(at));
-      const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds4_at(at + 4 * (BN * 2)));
-      bf[buf][ks][j] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    }
-  };
-  auto read_frags = [&](int buf, int st, int sta = -1) {
-#pragma unroll
-    for (int f = 0; f < KS * (TM + TN); ++f) frag_op(buf, st, f, sta);
-  };
-  // MFMA m of a step: m = (ks * TM + i) * TN + jj, with j = jj on even i and TN - 1 - jj on odd i
-  // (a snake over the blocks), so that consecutive MFMAs always share one operand register: the
-  // A fragment within a row of blocks, the B fragment across the turn. The part is power-limited
-  // on random operands and the MFMA's power grows with the operand bits that toggle between
-  // instructions: measured ~1 % faster than the plain row order at 4096^3, same result bits (every
-  // accumulator still receives its MFMAs in K order).
-  auto mfma_op = [&](int buf, int m) {
-    const int ks = m / (TM * TN), i = (m / TN) % TM, jj = m % TN, j = (i & 1) ? TN - 1 - jj : jj;
-    if constexpr (Cfg::MF16)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
-    else
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
-  };
+      return row * (BK * 2) + ((chunk ^ Cfg::swz_a(row)) * 16);
+    };
+    auto b_off = [&](int j, int krow) {
+      const int col = wn0 + MB * j + b_col_in;
+      return krow * (BN * 2) + (((col >> 3) ^ Cfg::swz_b(krow)) * 16) + (col & 7) * 2;
+    };
+    // Every k row one lane reads in a step (b_k_in, +4, +MK per substep) has the same swizzle (see
+    // swz_b): b_off(j, b_k_in + r) = b_off(j, b_k_in) + r * BN * 2. One LDS address per block, offset
+    // by the stage base, serves all of a step's transposing reads.
+    uint32_t b_tr[TN];
+  #pragma unroll
+    for (int j = 0; j < TN; ++j) b_tr[j] = sB_lds + static_cast<uint32_t>(b_off(j, b_k_in));
 
-  // Resident A: this tile's BM rows of X, scaled and cast to fp16, written as the stage images of
-  // all nk K steps (row r's logical 16-byte chunk c of step j at stage j, byte r * BK * 2 +
-  // ((c ^ swz_a(r)) * 16): where the DMA would put it), zeros past K and past M; s_scale[r] gets
-  // the row's scale. Wavefront w casts rows 8w .. 8w+7, all of their loads in flight at once.
-  auto cast_resident = [&](auto* xp) {
-    if constexpr (RESIDENT) {
-      using TX = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
-      constexpr int EPC = 16 / static_cast<int>(sizeof(TX));                  // elements per input chunk
-      constexpr int CM = (kResidentSteps * BK / EPC + kWave - 1) / kWave;      // input chunks per lane and row
-      constexpr int RPW = BM / Cfg::WAVES;                                     // rows per wavefront
-      constexpr int RB = RPW;                                                  // rows in flight
-      const int nch = K / EPC;
-      for (int b = 0; b < RPW; b += RB) {
-        u32x4 v[RB][CM];
-        float am[RB];
-#pragma unroll
-        for (int i = 0; i < RB; ++i) {
-          const int grow = m0 + wave * RPW + b + i;
-          const u32x4* xr = reinterpret_cast<const u32x4*>(xp + static_cast<size_t>(min(grow, M - 1)) * K);
-          am[i] = 0.f;
-#pragma unroll
-          for (int c = 0; c < CM; ++c) {
-            const int idx = lane + c * kWave;
-            v[i][c] = (grow < M && idx < nch) ? xr[idx] : u32x4{0u, 0u, 0u, 0u};
+    using AccT = std::conditional_t<Cfg::MF16, float4v, float16v>;
+    AccT acc[TM][TN];
+  #pragma unroll
+    for (int i = 0; i < TM; ++i)
+  #pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
+
+    // Fragments of one whole K step (BK/MK MFMA substeps), double-buffered across steps: the MFMAs
+    // of step j run on set j&1 while the LDS reads of step j+1 fill set (j+1)&1.
+    constexpr int KS = BK / MK;
+    half8 af[2][KS][TM], bf[2][KS][TN];
+    // Speculative A: the largest and smallest x this lane has multiplied, per fragment row i and per
+    // fp16 half of a dword (lane l's A fragments i are all of row wm0 + 32 i + l % 32). The IEEE
+    // maximum/minimum propagate a NaN, so a NaN counts as above the threshold, which only costs a
+    // recompute. Chains of two become v_pk_maximum3_f16 / v_pk_minimum3_f16: 4 VALU instructions per
+    // 8-value fragment.
+    half2v xmax[TM] = {}, xmin[TM] = {};
+    auto track_amax = [&](int buf) {
+      if constexpr (SPEC) {
+  #pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+  #pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            const half8 v = af[buf][ks][i];
+            const half2v d0 = __builtin_shufflevector(v, v, 0, 1), d1 = __builtin_shufflevector(v, v, 2, 3);
+            const half2v d2 = __builtin_shufflevector(v, v, 4, 5), d3 = __builtin_shufflevector(v, v, 6, 7);
+            xmax[i] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(xmax[i], d0), d1);
+            xmax[i] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(xmax[i], d2), d3);
+            xmin[i] = __builtin_elementwise_minimum(__builtin_elementwise_minimum(xmin[i], d0), d1);
+            xmin[i] = __builtin_elementwise_minimum(__builtin_elementwise_minimum(xmin[i], d2), d3);
           }
-        }
-#pragma unroll
-        for (int i = 0; i < RB; ++i)
-#pragma unroll
-          for (int c = 0; c < CM; ++c) am[i] = chunk_absmax(am[i], v[i][c], TX{});
-#pragma unroll
-        for (int i = 0; i < RB; ++i) am[i] = wave_max(am[i]);
-#pragma unroll
-        for (int i = 0; i < RB; ++i) {
-          const int r = wave * RPW + b + i;
-          int e;
-          float sc;
-          row_exponent(am[i], texp, e, sc);
-          if (lane == 0) s_scale[r] = sc;
-          unsigned char* row_base = &sA[0][0] + r * (BK * 2);
-          const int sw = Cfg::swz_a(r);
-#pragma unroll
-          for (int c = 0; c < CM; ++c) {
-            const int idx = lane + c * kWave;
-            if (idx < nch) {
-              if constexpr (EPC == 8) {
-                // elements 8 idx .. 8 idx + 7: step idx / 8, logical chunk idx % 8
-                *reinterpret_cast<u32x4*>(row_base + (idx >> 3) * Cfg::A_BYTES + (((idx & 7) ^ sw) << 4)) =
-                    cast_scaled(v[i][c], e, TX{});
-              } else {
-                // elements 4 idx .. 4 idx + 3: half idx % 2 of output chunk idx / 2
-                const int oc = idx >> 1;
-                *reinterpret_cast<u32x2*>(row_base + (oc >> 3) * Cfg::A_BYTES + (((oc & 7) ^ sw) << 4) + ((idx & 1) << 3)) =
-                    cast_scaled(v[i][c], e, TX{});
+      }
+    };
+    // The recomputation's cast: fp16_rne(x * 2^-e) of each fragment row, as one fp16 multiply by the
+    // row's factor 2^-e (0 for a row whose scale is +inf): the product is exact before rounding, and
+    // fp16 denormals are kept, so it is the rowscale cast's value bit for bit (e <= 24 here).
+    half2v fac[TM];
+    auto scale_frags = [&](int buf) {
+      if constexpr (SPEC) {
+  #pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+  #pragma unroll
+          for (int i = 0; i < TM; ++i)
+            af[buf][ks][i] *= __builtin_shufflevector(fac[i], fac[i], 0, 1, 0, 1, 0, 1, 0, 1);
+      }
+    };
+    // fragment read f of a step: f = ks * (TM + TN) + (i < TM ? i : TM + j)
+    // st: the ring stage of B (and of A); sta: A's stage where it differs (the resident-A tile keeps
+    // every K step's A image in its own stage)
+    auto frag_op = [&](int buf, int st, int f, int sta = -1) {
+      const int ks = f / (TM + TN), w = f % (TM + TN);
+      if (w < TM) {
+        af[buf][ks][w] = *reinterpret_cast<const half8*>(&sA[sta < 0 ? st : sta][a_off(w, ks)]);
+      } else if constexpr (PACKED_B) {
+        // B^T stored [n][k] like A: one 16-byte read gives lane l the k-run of column l%32.
+        const int j = w - TM;
+        const int row = wn0 + MB * j + frow;
+        const int chunk = ks * (MK / 8) + fk;
+        bf[buf][ks][j] = *reinterpret_cast<const half8*>(
+            &sB[st][row * (BK * 2) + ((chunk ^ Cfg::swz_a(row)) * 16)]);
+      } else {
+        const int j = w - TM;
+        const uint32_t at = b_tr[j] + st * Cfg::B_BYTES + ks * MK * (BN * 2);
+        const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds4_at(at));
+        const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds4_at(at + 4 * (BN * 2)));
+        bf[buf][ks][j] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    };
+    auto read_frags = [&](int buf, int st, int sta = -1) {
+  #pragma unroll
+      for (int f = 0; f < KS * (TM + TN); ++f) frag_op(buf, st, f, sta);
+    };
+    // MFMA m of a step: m = (ks * TM + i) * TN + jj, with j = jj on even i and TN - 1 - jj on odd i
+    // (a snake over the blocks), so that consecutive MFMAs always share one operand register: the
+    // A fragment within a row of blocks, the B fragment across the turn. The part is power-limited
+    // on random operands and the MFMA's power grows with the operand bits that toggle between
+    // instructions: measured ~1 % faster than the plain row order at 4096^3, same result bits (every
+    // accumulator still receives its MFMAs in K order).
+    auto mfma_op = [&](int buf, int m) {
+      const int ks = m / (TM * TN), i = (m / TN) % TM, jj = m % TN, j = (i & 1) ? TN - 1 - jj : jj;
+      if constexpr (Cfg::MF16)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
+      else
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[buf][ks][i], bf[buf][ks][j], acc[i][j], 0, 0, 0);
+    };
+
+    // Resident A: this tile's BM rows of X, scaled and cast to fp16, written as the stage images of
+    // all nk K steps (row r's logical 16-byte chunk c of step j at stage j, byte r * BK * 2 +
+    // ((c ^ swz_a(r)) * 16): where the DMA would put it), zeros past K and past M; s_scale[r] gets
+    // the row's scale. Wavefront w casts rows 8w .. 8w+7, all of their loads in flight at once.
+    auto cast_resident = [&](auto* xp) {
+      if constexpr (RESIDENT) {
+        using TX = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+        constexpr int EPC = 16 / static_cast<int>(sizeof(TX));                  // elements per input chunk
+        constexpr int CM = (kResidentSteps * BK / EPC + kWave - 1) / kWave;      // input chunks per lane and row
+        constexpr int RPW = BM / Cfg::WAVES;                                     // rows per wavefront
+        constexpr int RB = RPW;                                                  // rows in flight
+        const int nch = K / EPC;
+        for (int b = 0; b < RPW; b += RB) {
+          u32x4 v[RB][CM];
+          float am[RB];
+  #pragma unroll
+          for (int i = 0; i < RB; ++i) {
+            const int grow = m0 + wave * RPW + b + i;
+            const u32x4* xr = reinterpret_cast<const u32x4*>(xp + static_cast<size_t>(min(grow, M - 1)) * K);
+            am[i] = 0.f;
+  #pragma unroll
+            for (int c = 0; c < CM; ++c) {
+              const int idx = lane + c * kWave;
+              v[i][c] = (grow < M && idx < nch) ? xr[idx] : u32x4{0u, 0u, 0u, 0u};
+            }
+          }
+  #pragma unroll
+          for (int i = 0; i < RB; ++i)
+  #pragma unroll
+            for (int c = 0; c < CM; ++c) am[i] = chunk_absmax(am[i], v[i][c], TX{});
+  #pragma unroll
+          for (int i = 0; i < RB; ++i) am[i] = wave_max(am[i]);
+  #pragma unroll
+          for (int i = 0; i < RB; ++i) {
+            const int r = wave * RPW + b + i;
+            int e;
+            float sc;
+            row_exponent(am[i], texp, e, sc);
+            if (lane == 0) s_scale[r] = sc;
+            unsigned char* row_base = &sA[0][0] + r * (BK * 2);
+            const int sw = Cfg::swz_a(r);
+  #pragma unroll
+            for (int c = 0; c < CM; ++c) {
+              const int idx = lane + c * kWave;
+              if (idx < nch) {
+                if constexpr (EPC == 8) {
+                  // elements 8 idx .. 8 idx + 7: step idx / 8, logical chunk idx % 8
+                  *reinterpret_cast<u32x4*>(row_base + (idx >> 3) * Cfg::A_BYTES + (((idx & 7) ^ sw) << 4)) =
+                      cast_scaled(v[i][c], e, TX{});
+                } else {
+                  // elements 4 idx .. 4 idx + 3: half idx % 2 of output chunk idx / 2
+                  const int oc = idx >> 1;
+                  *reinterpret_cast<u32x2*>(row_base + (oc >> 3) * Cfg::A_BYTES + (((oc & 7) ^ sw) << 4) + ((idx & 1) << 3)) =
+                      cast_scaled(v[i][c], e, TX{});
+                }
               }
             }
           }
         }
-      }
-      // zeros for the columns past K in the last step (K % BK != 0)
-      const int oc0 = K / 8, oc1 = nk * (BK / 8);
-      for (int i = 0; i < RPW; ++i) {
-        const int r = wave * RPW + i;
-        unsigned char* row_base = &sA[0][0] + r * (BK * 2);
-        for (int oc = oc0 + lane; oc < oc1; oc += kWave)
-          *reinterpret_cast<u32x4*>(row_base + (oc >> 3) * Cfg::A_BYTES + (((oc & 7) ^ Cfg::swz_a(r)) << 4)) =
-              u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-
-  static_assert(NSTAGE >= 3, "three stages at least");
-  constexpr int NMFMA = KS * TM * TN, NFRAG = KS * (TM + TN), NDMA = Cfg::DMA_PER_STEP;
-  // ---- 4-wavefront tiles: a ring of NSTAGE stages ----
-  // During step j: MFMAs of step j (its fragments are already in registers, read during step j-1),
-  // LDS reads of step j+1, and DMA of step j+NSTAGE into stage j%NSTAGE -- the stage step j came
-  // from, which nobody reads any more. Before the barrier that ends step j, step j+2 must have
-  // landed (it is read during j+1): NSTAGE-2 younger steps of DMA may still be in flight, giving
-  // each DMA NSTAGE-1 steps to arrive. The three streams are cut into PARTS slices issued
-  // round-robin (DMA, MFMAs, LDS reads), so no wavefront front-loads its DMA and the memory pipes
-  // see a steady trickle between barriers.
-  constexpr int LAG = NSTAGE - 2;
-  // One pass of the K loop over [kbeg, kend) into acc, with A streamed through the ring (RES
-  // false) or cast into the resident stages first (RES true); RESCALE: the speculative path's
-  // recomputation, which scales the streamed A fragments by their rows' factors before use.
-  auto kloop4 = [&](auto resc, auto rescale) {
-    constexpr bool RES = decltype(resc)::value;
-    constexpr bool RESCALE = decltype(rescale)::value;
-    // DMA instructions per step: A and B, or B alone with resident A
-    constexpr int DMA0 = RES ? Cfg::A_INSTR : 0;
-    constexpr int PARTS = NDMA - DMA0;
-    if constexpr (RES) {
-      if (nk > 0) {
-#pragma unroll
-        for (int s = 0; s < NSTAGE; ++s) {
-          const int k0 = kbeg + s * BK;
-          const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
-#pragma unroll
-          for (int d = DMA0; d < NDMA; ++d) dma_op(s, k0, ra, rb, d);
+        // zeros for the columns past K in the last step (K % BK != 0)
+        const int oc0 = K / 8, oc1 = nk * (BK / 8);
+        for (int i = 0; i < RPW; ++i) {
+          const int r = wave * RPW + i;
+          unsigned char* row_base = &sA[0][0] + r * (BK * 2);
+          for (int oc = oc0 + lane; oc < oc1; oc += kWave)
+            *reinterpret_cast<u32x4*>(row_base + (oc >> 3) * Cfg::A_BYTES + (((oc & 7) ^ Cfg::swz_a(r)) << 4)) =
+                u32x4{0u, 0u, 0u, 0u};
         }
       }
-      // While B's first stages land: the cast of this tile's rows into the resident A stages.
-      if (x_f32) cast_resident(static_cast<const float*>(X));
-      else cast_resident(static_cast<const _Float16*>(X));
-    } else {
-      if (nk > 0) {
-#pragma unroll
-        for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
-      }
-    }
-    wait_dma_le<LAG * PARTS>();  // steps 0 and 1 have landed
-    __syncthreads();
-    if (nk > 0) read_frags(0, 0);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __syncthreads();  // every wavefront holds step 0 in registers: stage 0 may be refilled
-    // Step j on fragment buffer H (a compile-time constant, so two steps make one loop trip). The
-    // loop body has no branches: a conditional step or a conditional read inside it made the
-    // compiler copy accumulators between AGPRs and VGPRs on every trip (measured: ~3x slower
-    // steps). The last step's reads of step j+1 are harmless: they read a stage inside the ring
-    // (zeros or stale data) into the buffer no MFMA uses afterwards.
-    auto step = [&](auto hc, int j) {
-      constexpr int H = decltype(hc)::value;
-      const int kd = kbeg + (j + NSTAGE) * BK;
-      const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
-      // resident A: step j+1's own stage (the last step reads an in-range stage it does not use)
-      const int sta = RES ? (j + 1 < nk ? j + 1 : j) : -1;
-      const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
-      if constexpr (RESCALE) scale_frags(H);
-#pragma unroll
-      for (int p = 0; p < PARTS; ++p) {
-        dma_op(std_, kd, ra, rb, DMA0 + p);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(H, m);
-#pragma unroll
-        for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f, sta);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // step j's A fragments (streamed x), after the step's MFMAs have been issued on them
-      if constexpr (SPEC && !RES && !RESCALE) track_amax(H);
-      wait_dma_le<LAG * PARTS>();  // step j+2 has landed (this wavefront's part)
-      __syncthreads();            // ... every wavefront's part; step j+1 is in registers
     };
-    b_run = B + static_cast<size_t>(kbeg + NSTAGE * BK) * N + n0;
-    int it = 0;
-    for (; it + 1 < nk; it += 2) {
-      step(std::integral_constant<int, 0>{}, it);
-      step(std::integral_constant<int, 1>{}, it + 1);
-    }
-    if (it < nk) step(std::integral_constant<int, 0>{}, it);
-  };
-  if constexpr (Cfg::WAVES == 8) {
-    // Ping-pong schedule for two wavefronts per SIMD. Wavefronts 0-3 (group 0) and 4-7 (group 1)
-    // land one of each on every SIMD. Each wavefront alternates a memory phase M_j (fragment reads
-    // of step j from LDS, DMA of step j+D into the ring) and a compute phase C_j (the 16 MFMAs of
-    // step j), with a workgroup barrier after every phase; group 1 starts one phase late, so on
-    // every SIMD one wavefront streams MFMAs while the other one waits on memory.
-    //   Ring hazards, with D = NSTAGE - 1: the DMA issued in M_j writes stage (j+D)%NSTAGE, which
-    // last held step j-1; both groups read step j-1 in M_{j-1}, which ends at or before the barrier
-    // that opens M_j for either group. The fragment reads of M_j need every wavefront's DMA of
-    // step j: each wavefront waits for its own at the end of M_{j-1}, and the barrier after that
-    // phase publishes it to the group that reads next.
-    constexpr int D = NSTAGE - 1;
-    const int grp = wave >> 2;
-    if (nk > 0) {
-#pragma unroll
-      for (int s = 0; s < D; ++s) dma(s, kbeg + s * BK);
-    }
-    wait_dma_le<(D - 1) * NDMA>();  // step 0 has landed
-    b_run = B + static_cast<size_t>(kbeg + D * BK) * N + n0;
-    phase_barrier();
-    if (grp == 1) phase_barrier();
-    for (int j = 0; j < nk; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      {
-        // The memory phase interleaves its fragment reads (LDS) and its DMA issue (texture path):
-        // NFRAG / NDMA reads, then one DMA instruction, NDMA times, then any reads left over. On
-        // the 256x256 tile at 4096^3 (12 reads, 4 DMA) this ran 0.4-0.6 % faster than all reads
-        // before all DMA, with the same result bits; every form that issues a DMA before the
-        // first reads ran 1.5-3 % slower.
-        const int kd = kbeg + (j + D) * BK;
-        const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
-        constexpr int PER = NFRAG / NDMA;
-#pragma unroll
-        for (int d = 0; d < NDMA; ++d) {
-#pragma unroll
-          for (int f = d * PER; f < (d + 1) * PER; ++f) frag_op(0, j % NSTAGE, f);
-          dma_op((j + D) % NSTAGE, kd, ra, rb, d);
-        }
-#pragma unroll
-        for (int f = NDMA * PER; f < NFRAG; ++f) frag_op(0, j % NSTAGE, f);
-      }
-      wait_dma_le<(D - 1) * NDMA>();  // step j+1 has landed (this wavefront's part)
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // step j's fragments are in registers
-      phase_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int m = 0; m < NMFMA; ++m) mfma_op(0, m);
-      __builtin_amdgcn_sched_barrier(0);
-      phase_barrier();
-    }
-    if (grp == 0) phase_barrier();  // every wavefront passes the same number of barriers
-  } else {
-    if constexpr (RESIDENT) kloop4(std::true_type{}, std::false_type{});
-    else kloop4(std::false_type{}, std::false_type{});
-  }
-  wait_dma_le<0>();  // no DMA may still be writing LDS past this point
-  if (stamps && tid == 0) {
-    g_loop_clock[0] = __builtin_amdgcn_s_memtime() - clk_c0;
-    g_loop_clock[1] = __builtin_amdgcn_s_memrealtime() - clk_r0;
-  }
 
-  // ---- speculative A: recompute the tile where some |x| exceeded the threshold ----
-  bool respec = false;  // acc comes from the rescaled A, with the row scales in s_scale
-  auto zero_acc = [&]() {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
-  };
-  // max with a NaN in either operand giving NaN
-  auto nan_max = [](float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); };
-  // this lane's rows' |max| over the K range it has multiplied (lanes l and l ^ 32 hold the same
-  // row, different k), NaN where a NaN was seen
-  float ramax[TM];
-  int over = 0;  // some row of this slice exceeded the threshold or held a NaN (the workgroup agrees)
-  if constexpr (SPEC) {
-    // the largest fp16 value not above the threshold; a NaN fails the comparison
-    const float t = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(tbits)));
-    bool within = true;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      float a = nan_max(nan_max(static_cast<float>(xmax[i].x), static_cast<float>(xmax[i].y)),
-                        nan_max(-static_cast<float>(xmin[i].x), -static_cast<float>(xmin[i].y)));
-      a = nan_max(a, __shfl_xor(a, 32));
-      ramax[i] = a;
-      within = within && a <= t;
-    }
-    over = __syncthreads_or(within ? 0 : 1);
-  }
-  // With s_rowmax holding every row's |max| (NaN where a NaN was seen): the rows' exponents, exactly
-  // as the rowscale cast derives them, into s_scale (2^e) and this lane's factors fac (2^-e). A
-  // row with a NaN gets its |max| over all of K from x itself, NaN dropped as the cast drops it.
-  auto row_factors = [&]() {
-    if constexpr (SPEC) {
-      for (int r = wave; r < BM; r += Cfg::WAVES) {
-        const float v = s_rowmax[r];
-        if (v != v) {
-          float am = 0.f;
-          if (m0 + r < M) {
-            const u32x4* xr = reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m0 + r) * K);
-            for (int idx = lane; idx < K / 8; idx += kWave) am = chunk_absmax(am, xr[idx], _Float16{});
+    static_assert(NSTAGE >= 3, "three stages at least");
+    constexpr int NMFMA = KS * TM * TN, NFRAG = KS * (TM + TN), NDMA = Cfg::DMA_PER_STEP;
+    // ---- 4-wavefront tiles: a ring of NSTAGE stages ----
+    // During step j: MFMAs of step j (its fragments are already in registers, read during step j-1),
+    // LDS reads of step j+1, and DMA of step j+NSTAGE into stage j%NSTAGE -- the stage step j came
+    // from, which nobody reads any more. Before the barrier that ends step j, step j+2 must have
+    // landed (it is read during j+1): NSTAGE-2 younger steps of DMA may still be in flight, giving
+    // each DMA NSTAGE-1 steps to arrive. The three streams are cut into PARTS slices issued
+    // round-robin (DMA, MFMAs, LDS reads), so no wavefront front-loads its DMA and the memory pipes
+    // see a steady trickle between barriers.
+    constexpr int LAG = NSTAGE - 2;
+    // One pass of the K loop over [kbeg, kend) into acc, with A streamed through the ring (RES
+    // false) or cast into the resident stages first (RES true); RESCALE: the speculative path's
+    // recomputation, which scales the streamed A fragments by their rows' factors before use.
+    auto kloop4 = [&](auto resc, auto rescale) {
+      constexpr bool RES = decltype(resc)::value;
+      constexpr bool RESCALE = decltype(rescale)::value;
+      // DMA instructions per step: A and B, or B alone with resident A
+      constexpr int DMA0 = RES ? Cfg::A_INSTR : 0;
+      constexpr int PARTS = NDMA - DMA0;
+      if constexpr (RES) {
+        if (nk > 0) {
+  #pragma unroll
+          for (int s = 0; s < NSTAGE; ++s) {
+            const int k0 = kbeg + s * BK;
+            const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
+  #pragma unroll
+            for (int d = DMA0; d < NDMA; ++d) dma_op(s, k0, ra, rb, d);
           }
-          am = wave_max(am);
-          if (lane == 0) s_rowmax[r] = am;
+        }
+        // While B's first stages land: the cast of this tile's rows into the resident A stages.
+        if (x_f32) cast_resident(static_cast<const float*>(X));
+        else cast_resident(static_cast<const _Float16*>(X));
+      } else {
+        if (nk > 0) {
+  #pragma unroll
+          for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
         }
       }
+      wait_dma_le<LAG * PARTS>();  // steps 0 and 1 have landed
       __syncthreads();
-      if (tid < BM) {
-        int e;
-        float sc;
-        row_exponent(s_rowmax[tid], texp, e, sc);
-        s_scale[tid] = sc;
-        s_rowmax[tid] = e == kInfExp ? 0.f : ldexpf(1.f, -e);
+      if (nk > 0) read_frags(0, 0);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __syncthreads();  // every wavefront holds step 0 in registers: stage 0 may be refilled
+      // Step j on fragment buffer H (a compile-time constant, so two steps make one loop trip). The
+      // loop body has no branches: a conditional step or a conditional read inside it made the
+      // compiler copy accumulators between AGPRs and VGPRs on every trip (measured: ~3x slower
+      // steps). The last step's reads of step j+1 are harmless: they read a stage inside the ring
+      // (zeros or stale data) into the buffer no MFMA uses afterwards.
+      auto step = [&](auto hc, int j) {
+        constexpr int H = decltype(hc)::value;
+        const int kd = kbeg + (j + NSTAGE) * BK;
+        const int std_ = j % NSTAGE, stf = (j + 1) % NSTAGE;
+        // resident A: step j+1's own stage (the last step reads an in-range stage it does not use)
+        const int sta = RES ? (j + 1 < nk ? j + 1 : j) : -1;
+        const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
+        if constexpr (RESCALE) scale_frags(H);
+  #pragma unroll
+        for (int p = 0; p < PARTS; ++p) {
+          dma_op(std_, kd, ra, rb, DMA0 + p);
+          __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+          for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(H, m);
+  #pragma unroll
+          for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f, sta);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // step j's A fragments (streamed x), after the step's MFMAs have been issued on them
+        if constexpr (SPEC && !RES && !RESCALE) track_amax(H);
+        wait_dma_le<LAG * PARTS>();  // step j+2 has landed (this wavefront's part)
+        __syncthreads();            // ... every wavefront's part; step j+1 is in registers
+      };
+      b_run = B + static_cast<size_t>(kbeg + NSTAGE * BK) * N + n0;
+      int it = 0;
+      for (; it + 1 < nk; it += 2) {
+        step(std::integral_constant<int, 0>{}, it);
+        step(std::integral_constant<int, 1>{}, it + 1);
       }
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const _Float16 f = static_cast<_Float16>(s_rowmax[wm0 + 32 * i + (lane & 31)]);
-        fac[i] = half2v{f, f};
-      }
-    }
-  };
-  // the wavefronts of the first column hold every row once: lanes < 32 write them
-  const bool row_writer = wave % Cfg::WGN == 0 && lane < 32;
-  // a recomputation is remembered for the weight (the host routes its next calls around it)
-  auto note_miss = [&]() {
-    if (spec_miss != nullptr && tid == 0) __hip_atomic_store(spec_miss, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  };
-  if constexpr (SPEC && !SPLITK) {
-    if (over) {
-      respec = true;
-      note_miss();
-      if (row_writer) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) s_rowmax[wm0 + 32 * i + lane] = ramax[i];
-      }
-      __syncthreads();
-      row_factors();
-      zero_acc();
-      kloop4(std::false_type{}, std::true_type{});
-      wait_dma_le<0>();
-    }
-  }
-
-  // ---- split-K: publish this slice, let the last slice reduce ----
-  if constexpr (SPLITK) {
-    constexpr uint32_t TILE_BYTES = BM * BN * 4;
-    // Each wavefront stores its accumulators in its own register order: slot s of the wavefront is
-    // float4 piece q of accumulator (i, j), s = (i * TN + j) * QV + q.
-    constexpr int QV = sizeof(AccT) / sizeof(float4v);  // 4 for 32x32 blocks, 1 for 16x16 blocks
-    constexpr int SLOTS = TM * TN * QV;
-    auto piece = [&](int s) -> float4v {
-      const int b = s / QV, q = s % QV;
-      if constexpr (QV == 1) {
-        return acc[b / TN][b % TN];
-      } else {
-        const AccT& a = acc[b / TN][b % TN];
-        return float4v{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
-      }
+      if (it < nk) step(std::integral_constant<int, 0>{}, it);
     };
-    auto set_piece = [&](int s, float4v v) {
-      const int b = s / QV, q = s % QV;
-      if constexpr (QV == 1) {
-        acc[b / TN][b % TN] = v;
-      } else {
-        AccT& a = acc[b / TN][b % TN];
-        a[4 * q] = v.x;
-        a[4 * q + 1] = v.y;
-        a[4 * q + 2] = v.z;
-        a[4 * q + 3] = v.w;
+    if constexpr (Cfg::WAVES == 8) {
+      // Ping-pong schedule for two wavefronts per SIMD. Wavefronts 0-3 (group 0) and 4-7 (group 1)
+      // land one of each on every SIMD. Each wavefront alternates a memory phase M_j (fragment reads
+      // of step j from LDS, DMA of step j+D into the ring) and a compute phase C_j (the 16 MFMAs of
+      // step j), with a workgroup barrier after every phase; group 1 starts one phase late, so on
+      // every SIMD one wavefront streams MFMAs while the other one waits on memory.
+      //   Ring hazards, with D = NSTAGE - 1: the DMA issued in M_j writes stage (j+D)%NSTAGE, which
+      // last held step j-1; both groups read step j-1 in M_{j-1}, which ends at or before the barrier
+      // that opens M_j for either group. The fragment reads of M_j need every wavefront's DMA of
+      // step j: each wavefront waits for its own at the end of M_{j-1}, and the barrier after that
+      // phase publishes it to the group that reads next.
+      constexpr int D = NSTAGE - 1;
+      const int grp = wave >> 2;
+      if (nk > 0) {
+  #pragma unroll
+        for (int s = 0; s < D; ++s) dma(s, kbeg + s * BK);
       }
-    };
-    const __amdgpu_buffer_rsrc_t slices =
-        coherent_rsrc(part + static_cast<size_t>(tile) * ksplit * (BM * BN), static_cast<uint32_t>(ksplit) * TILE_BYTES);
-    auto slot_off = [&](int z, int s) {
-      return static_cast<uint32_t>(z) * TILE_BYTES + static_cast<uint32_t>((wave * SLOTS + s) * 64 + lane) * 16u;
-    };
-    // the speculative path's rows' |max| of slice z: the first BM floats of its partial tile
-    auto rowmax_slot = [&](int zz) { return part + (static_cast<size_t>(tile) * ksplit + zz) * (BM * BN); };
-    if (SPEC && over) {
-      // the last slice recomputes this tile: publish the rows' |max| in place of the partial tile
-      if (row_writer) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) store_coherent(rowmax_slot(z) + wm0 + 32 * i + lane, ramax[i]);
+      wait_dma_le<(D - 1) * NDMA>();  // step 0 has landed
+      b_run = B + static_cast<size_t>(kbeg + D * BK) * N + n0;
+      phase_barrier();
+      if (grp == 1) phase_barrier();
+      for (int j = 0; j < nk; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        {
+          // The memory phase interleaves its fragment reads (LDS) and its DMA issue (texture path):
+          // NFRAG / NDMA reads, then one DMA instruction, NDMA times, then any reads left over. On
+          // the 256x256 tile at 4096^3 (12 reads, 4 DMA) this ran 0.4-0.6 % faster than all reads
+          // before all DMA, with the same result bits; every form that issues a DMA before the
+          // first reads ran 1.5-3 % slower.
+          const int kd = kbeg + (j + D) * BK;
+          const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
+          constexpr int PER = NFRAG / NDMA;
+  #pragma unroll
+          for (int d = 0; d < NDMA; ++d) {
+  #pragma unroll
+            for (int f = d * PER; f < (d + 1) * PER; ++f) frag_op(0, j % NSTAGE, f);
+            dma_op((j + D) % NSTAGE, kd, ra, rb, d);
+          }
+  #pragma unroll
+          for (int f = NDMA * PER; f < NFRAG; ++f) frag_op(0, j % NSTAGE, f);
+        }
+        wait_dma_le<(D - 1) * NDMA>();  // step j+1 has landed (this wavefront's part)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // step j's fragments are in registers
+        phase_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+        for (int m = 0; m < NMFMA; ++m) mfma_op(0, m);
+        __builtin_amdgcn_sched_barrier(0);
+        phase_barrier();
       }
+      if (grp == 0) phase_barrier();  // every wavefront passes the same number of barriers
     } else {
-#pragma unroll
-      for (int s = 0; s < SLOTS; ++s) store_coherent4(slices, slot_off(z, s), piece(s));
+      if constexpr (RESIDENT) kloop4(std::true_type{}, std::false_type{});
+      else kloop4(std::false_type{}, std::false_type{});
     }
+    wait_dma_le<0>();  // no DMA may still be writing LDS past this point
+    if (stamps && tid == 0) {
+      g_loop_clock[0] = __builtin_amdgcn_s_memtime() - clk_c0;
+      g_loop_clock[1] = __builtin_amdgcn_s_memrealtime() - clk_r0;
+    }
+
+    // ---- speculative A: recompute the tile where some |x| exceeded the threshold ----
+    bool respec = false;  // acc comes from the rescaled A, with the row scales in s_scale
+    auto zero_acc = [&]() {
+  #pragma unroll
+      for (int i = 0; i < TM; ++i)
+  #pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
+    };
+    // max with a NaN in either operand giving NaN
+    auto nan_max = [](float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); };
+    // this lane's rows' |max| over the K range it has multiplied (lanes l and l ^ 32 hold the same
+    // row, different k), NaN where a NaN was seen
+    float ramax[TM];
+    int over = 0;  // some row of this slice exceeded the threshold or held a NaN (the workgroup agrees)
     if constexpr (SPEC) {
-      const uint32_t total = arrive_add_coherent(counters + tile * kCounterStride,
-                                                 1u + (over ? (1u << (kSpecShift + z)) : 0u));
-      if ((total & ((1u << kSpecShift) - 1u)) != static_cast<uint32_t>(ksplit)) return;
-      respec = (total >> kSpecShift) != 0u;
-      if (respec) {
-        // a row's |max| over K: the largest over the slices that saw a value above the threshold
-        // (the others hold none, so they cannot raise a row's exponent above 0)
-        const uint32_t mask = total >> kSpecShift;
-        if (tid < BM) {
-          float m = 0.f;
-          for (int zz = 0; zz < ksplit; ++zz)
-            if ((mask >> zz) & 1u) m = nan_max(m, load_coherent(rowmax_slot(zz) + tid));
-          s_rowmax[tid] = m;
+      // the largest fp16 value not above the threshold; a NaN fails the comparison
+      const float t = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(tbits)));
+      bool within = true;
+  #pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        float a = nan_max(nan_max(static_cast<float>(xmax[i].x), static_cast<float>(xmax[i].y)),
+                          nan_max(-static_cast<float>(xmin[i].x), -static_cast<float>(xmin[i].y)));
+        a = nan_max(a, __shfl_xor(a, 32));
+        ramax[i] = a;
+        within = within && a <= t;
+      }
+      over = __syncthreads_or(within ? 0 : 1);
+    }
+    // With s_rowmax holding every row's |max| (NaN where a NaN was seen): the rows' exponents, exactly
+    // as the rowscale cast derives them, into s_scale (2^e) and this lane's factors fac (2^-e). A
+    // row with a NaN gets its |max| over all of K from x itself, NaN dropped as the cast drops it.
+    auto row_factors = [&]() {
+      if constexpr (SPEC) {
+        for (int r = wave; r < BM; r += Cfg::WAVES) {
+          const float v = s_rowmax[r];
+          if (v != v) {
+            float am = 0.f;
+            if (m0 + r < M) {
+              const u32x4* xr = reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m0 + r) * K);
+              for (int idx = lane; idx < K / 8; idx += kWave) am = chunk_absmax(am, xr[idx], _Float16{});
+            }
+            am = wave_max(am);
+            if (lane == 0) s_rowmax[r] = am;
+          }
         }
         __syncthreads();
+        if (tid < BM) {
+          int e;
+          float sc;
+          row_exponent(s_rowmax[tid], texp, e, sc);
+          s_scale[tid] = sc;
+          s_rowmax[tid] = e == kInfExp ? 0.f : ldexpf(1.f, -e);
+        }
+        __syncthreads();
+  #pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const _Float16 f = static_cast<_Float16>(s_rowmax[wm0 + 32 * i + (lane & 31)]);
+          fac[i] = half2v{f, f};
+        }
       }
-    } else {
-      if (!arrive_last_coherent(counters + tile * kCounterStride, static_cast<uint32_t>(ksplit))) return;
-    }
-    // Slices are added in slice order (every slice, this one's included, is read back from the
-    // workspace), so each output is the same sum whichever slice arrives last.
-    if (SPEC && respec) {
-      // Some slice's A exceeded the threshold: recompute every slice with the rescaled A and add
-      // them in slice order, exactly as the reduction below adds the published slices.
-      if constexpr (SPEC) {
-        static_assert(SLOTS <= 16, "the 4-wavefront tiles");
+    };
+    // the wavefronts of the first column hold every row once: lanes < 32 write them
+    const bool row_writer = wave % Cfg::WGN == 0 && lane < 32;
+    // a recomputation is remembered for the weight (the host routes its next calls around it)
+    auto note_miss = [&]() {
+      if (spec_miss != nullptr && tid == 0) __hip_atomic_store(spec_miss, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    };
+    if constexpr (SPEC && !SPLITK) {
+      if (over) {
+        respec = true;
         note_miss();
+        if (row_writer) {
+  #pragma unroll
+          for (int i = 0; i < TM; ++i) s_rowmax[wm0 + 32 * i + lane] = ramax[i];
+        }
+        __syncthreads();
         row_factors();
-        float4v sum[SLOTS];
-#pragma unroll
-        for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
-        for (int zz = 0; zz < ksplit; ++zz) {
-          kbeg = zz * kchunk;
-          kend = min(K, kbeg + kchunk);
-          nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
-          zero_acc();
-          kloop4(std::false_type{}, std::true_type{});
-          wait_dma_le<0>();
-#pragma unroll
-          for (int s = 0; s < SLOTS; ++s) sum[s] += piece(s);
-        }
-#pragma unroll
-        for (int s = 0; s < SLOTS; ++s) set_piece(s, sum[s]);
-      }
-    } else if constexpr (SLOTS <= 16) {
-      // ZB slices' loads in flight at a time
-      constexpr int ZB = (128 / (SLOTS * 4)) < 1 ? 1 : ((128 / (SLOTS * 4)) > 8 ? 8 : (128 / (SLOTS * 4)));
-      float4v sum[SLOTS];
-#pragma unroll
-      for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
-      for (int z0 = 0; z0 < ksplit; z0 += ZB) {
-        float4v v[ZB][SLOTS];
-#pragma unroll
-        for (int b = 0; b < ZB; ++b)
-#pragma unroll
-          for (int s = 0; s < SLOTS; ++s)
-            v[b][s] = z0 + b < ksplit ? load_coherent4(slices, slot_off(z0 + b, s)) : float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int b = 0; b < ZB; ++b)
-#pragma unroll
-          for (int s = 0; s < SLOTS; ++s)
-            if (z0 + b < ksplit) sum[s] += v[b][s];
-      }
-#pragma unroll
-      for (int s = 0; s < SLOTS; ++s) set_piece(s, sum[s]);
-    } else {
-      // The 256x256 tile: its accumulators fill most of the register file, so the sums build up in
-      // the accumulators themselves, kCh slots at a time, two slices' loads in flight.
-      constexpr int kCh = 8;
-      static_assert(SLOTS % kCh == 0, "whole chunks");
-#pragma unroll
-      for (int c0 = 0; c0 < SLOTS; c0 += kCh) {
-        float4v s[kCh];
-#pragma unroll
-        for (int q = 0; q < kCh; ++q) s[q] = float4v{0.f, 0.f, 0.f, 0.f};
-        for (int z0 = 0; z0 < ksplit; z0 += 2) {
-          float4v v0[kCh], v1[kCh];
-#pragma unroll
-          for (int q = 0; q < kCh; ++q) {
-            v0[q] = load_coherent4(slices, slot_off(z0, c0 + q));
-            v1[q] = z0 + 1 < ksplit ? load_coherent4(slices, slot_off(z0 + 1, c0 + q)) : float4v{0.f, 0.f, 0.f, 0.f};
-          }
-#pragma unroll
-          for (int q = 0; q < kCh; ++q) {
-            s[q] += v0[q];
-            if (z0 + 1 < ksplit) s[q] += v1[q];
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < kCh; ++q) set_piece(c0 + q, s[q]);
+        zero_acc();
+        kloop4(std::false_type{}, std::true_type{});
+        wait_dma_le<0>();
       }
     }
-    reset_counter(counters + tile * kCounterStride);
-  }
 
-  // ---- epilogue: C = rscale[row] * acc + bias[col] ----
-  // Each wavefront moves its accumulators, one 32x32 region at a time, through a private 4 KB LDS
-  // scratch so that every lane ends up with 4 consecutive columns of one row: the result leaves in
-  // 16-byte (fp32) or 8-byte (fp16) stores, 4x fewer store instructions than one value per lane.
-  //   32x32x16 layout (a region is one block): lane l, register r -> column l%32, row
-  //   8*(r/4) + 4*(l/32) + r%4. Rows R and R+4 meet in one write; storing row R at physical row
-  //   R ^ ((R >> 2) & 1) gives them different bank halves.
-  //   16x16x32 layout (a region is 2x2 blocks a, b): lane l, register r -> column 16b + l%16, row
-  //   16a + 4*(l/16) + r. One write covers rows 4g + r of the four 16-lane groups g; the same row
-  //   swizzle plus column ^ 16*((R >> 3) & 1) puts the four groups on four distinct 16-bank ranges.
-  // The read-back (two rows of 8 lanes per 16 lanes) hits both bank halves whole in either layout.
-  __syncthreads();  // every wavefront's DMA has drained: the stages are free for scratch
-  float* scr = reinterpret_cast<float*>(&sB[0][0] + wave * 4096);
-  static_assert(Cfg::B_BYTES * NSTAGE >= 4096 * Cfg::WAVES, "scratch fits in the B stages");
-  auto phys = [](int row, int col) {
-    return (row ^ ((row >> 2) & 1)) * 32 + (Cfg::MF16 ? (col ^ (16 * ((row >> 3) & 1))) : col);
-  };
-#pragma unroll
-  for (int ri = 0; ri < Cfg::WTM / 32; ++ri) {
-#pragma unroll
-    for (int rj = 0; rj < Cfg::WTN / 32; ++rj) {
-      if constexpr (Cfg::MF16) {
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) scr[phys(16 * a + 4 * fk + r, 16 * b + frow)] = acc[2 * ri + a][2 * rj + b][r];
+    // ---- split-K: publish this slice, let the last slice reduce ----
+    if constexpr (SPLITK) {
+      constexpr uint32_t TILE_BYTES = BM * BN * 4;
+      // Each wavefront stores its accumulators in its own register order: slot s of the wavefront is
+      // float4 piece q of accumulator (i, j), s = (i * TN + j) * QV + q.
+      constexpr int QV = sizeof(AccT) / sizeof(float4v);  // 4 for 32x32 blocks, 1 for 16x16 blocks
+      constexpr int SLOTS = TM * TN * QV;
+      auto piece = [&](int s) -> float4v {
+        const int b = s / QV, q = s % QV;
+        if constexpr (QV == 1) {
+          return acc[b / TN][b % TN];
+        } else {
+          const AccT& a = acc[b / TN][b % TN];
+          return float4v{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+        }
+      };
+      auto set_piece = [&](int s, float4v v) {
+        const int b = s / QV, q = s % QV;
+        if constexpr (QV == 1) {
+          acc[b / TN][b % TN] = v;
+        } else {
+          AccT& a = acc[b / TN][b % TN];
+          a[4 * q] = v.x;
+          a[4 * q + 1] = v.y;
+          a[4 * q + 2] = v.z;
+          a[4 * q + 3] = v.w;
+        }
+      };
+      const __amdgpu_buffer_rsrc_t slices =
+          coherent_rsrc(part + static_cast<size_t>(tile) * ksplit * (BM * BN), static_cast<uint32_t>(ksplit) * TILE_BYTES);
+      auto slot_off = [&](int z, int s) {
+        return static_cast<uint32_t>(z) * TILE_BYTES + static_cast<uint32_t>((wave * SLOTS + s) * 64 + lane) * 16u;
+      };
+      // the speculative path's rows' |max| of slice z: the first BM floats of its partial tile
+      auto rowmax_slot = [&](int zz) { return part + (static_cast<size_t>(tile) * ksplit + zz) * (BM * BN); };
+      if (SPEC && over) {
+        // the last slice recomputes this tile: publish the rows' |max| in place of the partial tile
+        if (row_writer) {
+  #pragma unroll
+          for (int i = 0; i < TM; ++i) store_coherent(rowmax_slot(z) + wm0 + 32 * i + lane, ramax[i]);
+        }
       } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) scr[phys(8 * (r >> 2) + 4 * fk + (r & 3), frow)] = acc[ri][rj][r];
+  #pragma unroll
+        for (int s = 0; s < SLOTS; ++s) store_coherent4(slices, slot_off(z, s), piece(s));
       }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int id = lane + 64 * q;
-        const int row = id >> 3, c4 = (id & 7) * 4;
-        float4v v = *reinterpret_cast<const float4v*>(&scr[phys(row, c4)]);
-        const int grow = m0 + wm0 + 32 * ri + row;
-        const int gcol = n0 + wn0 + 32 * rj + c4;
-        if (grow < M && gcol < N) {  // N % 8 == 0: a 4-column chunk is all in or all out
-          const float rs = (RESIDENT || respec) ? s_scale[grow - m0]
-                                                : (SPEC ? 1.f : (rscale != nullptr ? rscale[grow] : 1.f));
-          const float4v b = bias != nullptr ? float4v{bias[gcol], bias[gcol + 1], bias[gcol + 2], bias[gcol + 3]}
-                                            : float4v{0.f, 0.f, 0.f, 0.f};
-          v = v * rs + b;
-          if constexpr (OUT_F16) {
-            const half4 h = {static_cast<_Float16>(v.x), static_cast<_Float16>(v.y), static_cast<_Float16>(v.z),
-                             static_cast<_Float16>(v.w)};
-            *reinterpret_cast<half4*>(static_cast<_Float16*>(Cv) + static_cast<size_t>(grow) * N + gcol) = h;
-          } else {
-            *reinterpret_cast<float4v*>(static_cast<float*>(Cv) + static_cast<size_t>(grow) * N + gcol) = v;
+      if constexpr (SPEC) {
+        const uint32_t total = arrive_add_coherent(counters + tile * kCounterStride,
+                                                   1u + (over ? (1u << (kSpecShift + z)) : 0u));
+        if ((total & ((1u << kSpecShift) - 1u)) != static_cast<uint32_t>(ksplit)) return;
+        respec = (total >> kSpecShift) != 0u;
+        if (respec) {
+          // a row's |max| over K: the largest over the slices that saw a value above the threshold
+          // (the others hold none, so they cannot raise a row's exponent above 0)
+          const uint32_t mask = total >> kSpecShift;
+          if (tid < BM) {
+            float m = 0.f;
+            for (int zz = 0; zz < ksplit; ++zz)
+              if ((mask >> zz) & 1u) m = nan_max(m, load_coherent(rowmax_slot(zz) + tid));
+            s_rowmax[tid] = m;
+          }
+          __syncthreads();
+        }
+      } else {
+        if (!arrive_last_coherent(counters + tile * kCounterStride, static_cast<uint32_t>(ksplit))) return;
+      }
+      // Slices are added in slice order (every slice, this one's included, is read back from the
+      // workspace), so each output is the same sum whichever slice arrives last.
+      if (SPEC && respec) {
+        // Some slice's A exceeded the threshold: recompute every slice with the rescaled A and add
+        // them in slice order, exactly as the reduction below adds the published slices.
+        if constexpr (SPEC) {
+          static_assert(SLOTS <= 16, "the 4-wavefront tiles");
+          note_miss();
+          row_factors();
+          float4v sum[SLOTS];
+  #pragma unroll
+          for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
+          for (int zz = 0; zz < ksplit; ++zz) {
+            kbeg = zz * kchunk;
+            kend = min(K, kbeg + kchunk);
+            nk = kend > kbeg ? ceil_div(kend - kbeg, BK) : 0;
+            zero_acc();
+            kloop4(std::false_type{}, std::true_type{});
+            wait_dma_le<0>();
+  #pragma unroll
+            for (int s = 0; s < SLOTS; ++s) sum[s] += piece(s);
+          }
+  #pragma unroll
+          for (int s = 0; s < SLOTS; ++s) set_piece(s, sum[s]);
+        }
+      } else if constexpr (SLOTS <= 16) {
+        // ZB slices' loads in flight at a time
+        constexpr int ZB = (128 / (SLOTS * 4)) < 1 ? 1 : ((128 / (SLOTS * 4)) > 8 ? 8 : (128 / (SLOTS * 4)));
+        float4v sum[SLOTS];
+  #pragma unroll
+        for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
+        for (int z0 = 0; z0 < ksplit; z0 += ZB) {
+          float4v v[ZB][SLOTS];
+  #pragma unroll
+          for (int b = 0; b < ZB; ++b)
+  #pragma unroll
+            for (int s = 0; s < SLOTS; ++s)
+              v[b][s] = z0 + b < ksplit ? load_coherent4(slices, slot_off(z0 + b, s)) : float4v{0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+          for (int b = 0; b < ZB; ++b)
+  #pragma unroll
+            for (int s = 0; s < SLOTS; ++s)
+              if (z0 + b < ksplit) sum[s] += v[b][s];
+        }
+  #pragma unroll
+        for (int s = 0; s < SLOTS; ++s) set_piece(s, sum[s]);
+      } else {
+        // The 256x256 tile: its accumulators fill most of the register file, so the sums build up in
+        // the accumulators themselves, kCh slots at a time, two slices' loads in flight.
+        constexpr int kCh = 8;
+        static_assert(SLOTS % kCh == 0, "whole chunks");
+  #pragma unroll
+        for (int c0 = 0; c0 < SLOTS; c0 += kCh) {
+          float4v s[kCh];
+  #pragma unroll
+          for (int q = 0; q < kCh; ++q) s[q] = float4v{0.f, 0.f, 0.f, 0.f};
+          for (int z0 = 0; z0 < ksplit; z0 += 2) {
+            float4v v0[kCh], v1[kCh];
+  #pragma unroll
+            for (int q = 0; q < kCh; ++q) {
+              v0[q] = load_coherent4(slices, slot_off(z0, c0 + q));
+              v1[q] = z0 + 1 < ksplit ? load_coherent4(slices, slot_off(z0 + 1, c0 + q)) : float4v{0.f, 0.f, 0.f, 0.f};
+            }
+  #pragma unroll
+            for (int q = 0; q < kCh; ++q) {
+              s[q] += v0[q];
+              if (z0 + 1 < ksplit) s[q] += v1[q];
+            }
+          }
+  #pragma unroll
+          for (int q = 0; q < kCh; ++q) set_piece(c0 + q, s[q]);
+        }
+      }
+      reset_counter(counters + tile * kCounterStride);
+    }
+
+    // ---- epilogue: C = rscale[row] * acc + bias[col] ----
+    // Each wavefront moves its accumulators, one 32x32 region at a time, through a private 4 KB LDS
+    // scratch so that every lane ends up with 4 consecutive columns of one row: the result leaves in
+    // 16-byte (fp32) or 8-byte (fp16) stores, 4x fewer store instructions than one value per lane.
+    //   32x32x16 layout (a region is one block): lane l, register r -> column l%32, row
+    //   8*(r/4) + 4*(l/32) + r%4. Rows R and R+4 meet in one write; storing row R at physical row
+    //   R ^ ((R >> 2) & 1) gives them different bank halves.
+    //   16x16x32 layout (a region is 2x2 blocks a, b): lane l, register r -> column 16b + l%16, row
+    //   16a + 4*(l/16) + r. One write covers rows 4g + r of the four 16-lane groups g; the same row
+    //   swizzle plus column ^ 16*((R >> 3) & 1) puts the four groups on four distinct 16-bank ranges.
+    // The read-back (two rows of 8 lanes per 16 lanes) hits both bank halves whole in either layout.
+    __syncthreads();  // every wavefront's DMA has drained: the stages are free for scratch
+    float* scr = reinterpret_cast<float*>(&sB[0][0] + wave * 4096);
+    static_assert(Cfg::B_BYTES * NSTAGE >= 4096 * Cfg::WAVES, "scratch fits in the B stages");
+    auto phys = [](int row, int col) {
+      return (row ^ ((row >> 2) & 1)) * 32 + (Cfg::MF16 ? (col ^ (16 * ((row >> 3) & 1))) : col);
+    };
+  #pragma unroll
+    for (int ri = 0; ri < Cfg::WTM / 32; ++ri) {
+  #pragma unroll
+      for (int rj = 0; rj < Cfg::WTN / 32; ++rj) {
+        if constexpr (Cfg::MF16) {
+  #pragma unroll
+          for (int a = 0; a < 2; ++a)
+  #pragma unroll
+            for (int b = 0; b < 2; ++b)
+  #pragma unroll
+              for (int r = 0; r < 4; ++r) scr[phys(16 * a + 4 * fk + r, 16 * b + frow)] = acc[2 * ri + a][2 * rj + b][r];
+        } else {
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) scr[phys(8 * (r >> 2) + 4 * fk + (r & 3), frow)] = acc[ri][rj][r];
+        }
+  #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int id = lane + 64 * q;
+          const int row = id >> 3, c4 = (id & 7) * 4;
+          float4v v = *reinterpret_cast<const float4v*>(&scr[phys(row, c4)]);
+          const int grow = m0 + wm0 + 32 * ri + row;
+          const int gcol = n0 + wn0 + 32 * rj + c4;
+          if (grow < M && gcol < N) {  // N % 8 == 0: a 4-column chunk is all in or all out
+            const float rs = (RESIDENT || respec) ? s_scale[grow - m0]
+                                                  : (SPEC ? 1.f : (rscale != nullptr ? rscale[grow] : 1.f));
+            const float4v b = bias != nullptr ? float4v{bias[gcol], bias[gcol + 1], bias[gcol + 2], bias[gcol + 3]}
+                                              : float4v{0.f, 0.f, 0.f, 0.f};
+            v = v * rs + b;
+            if constexpr (OUT_F16) {
+              const half4 h = {static_cast<_Float16>(v.x), static_cast<_Float16>(v.y), static_cast<_Float16>(v.z),
+                               static_cast<_Float16>(v.w)};
+              *reinterpret_cast<half4*>(static_cast<_Float16*>(Cv) + static_cast<size_t>(grow) * N + gcol) = h;
+            } else {
+              *reinterpret_cast<float4v*>(static_cast<float*>(Cv) + static_cast<size_t>(grow) * N + gcol) = v;
+            }
           }
         }
       }
     }
+    // the stages (and the epilogue scratch in them) are free before the next tile's DMA
+    if (work + static_cast<int>(gridDim.x) < ntiles) __syncthreads();
   }
 }
 
@@ -1269,8 +1280,13 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
     counters = counters_in;
     part = static_cast<float*>(ws);
   }
-  const dim3 grid(static_cast<unsigned>(p.ntm * p.ntn), static_cast<unsigned>(ks.ksplit)),
-      block(p.tile == Tile::T256 || p.tile == Tile::T256N ? Cfg256::THREADS : 256);
+  // The unsplit 256-row tiles hold one workgroup per CU: past one round, a persistent grid of one
+  // workgroup per CU (a multiple of 8, so each keeps its XCD's tile range) walks the tiles.
+  const bool big = p.tile == Tile::T256 || p.tile == Tile::T256N;
+  const long ntiles = static_cast<long>(p.ntm) * p.ntn;
+  const long persist = num_cus >= 8 ? num_cus / 8 * 8 : 8;
+  const long gx = big && ks.ksplit == 1 && ntiles > persist ? persist : ntiles;
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(ks.ksplit)), block(big ? Cfg256::THREADS : 256);
   const auto* a = reinterpret_cast<const _Float16*>(A);
   const auto* b = reinterpret_cast<const _Float16*>(B);
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -9,9 +9,10 @@ exactly as configured.
   tile split twice (64x4096x11008), the 128x128 tile unsplit and split with an odd number of K
   steps and a ragged last step, and the 32x128 tile of C3. The packed-weight 256x256 and 256x128
   tiles the planner falls back to when no 4-wavefront grid fits one round (M >= 512, long K, large
-  N) run unsplit. The tile each case runs on is read from
-  the library's split-buffer sizes, so a plan change that moves a case to another tile fails here
-  instead of silently dropping that tile from the tests.
+  N) run unsplit; past 256 tiles their grid is persistent (one workgroup per CU walking several
+  tiles), here with ragged tile counts and at the BERT-base linear shapes (sampled rows). The tile
+  each case runs on is read from the library's split-buffer sizes, so a plan change that moves a
+  case to another tile fails here instead of silently dropping that tile from the tests.
 * The fp16-output golden fixtures (exact rational results, tests/golden/make_golden.py).
 
 Every result is checked against the fp64 oracle: relative Frobenius error <= 1e-3 on the GEMM
@@ -93,6 +94,8 @@ ROUTES = [
     (384, 4056, 3072, (128, 128), 3),    # split: slices of 44, 44 and 39 K steps, the last one ragged
     (768, 4096, 11008, (256, 256), 1),   # no 4-wavefront grid fits one round: packed 256x256 tiles
     (512, 4096, 11008, (256, 128), 1),   # ... packed 256x128 tiles where their grid fits one round
+    (2560, 512, 8192, (256, 256), 1),    # 320 tiles: a persistent grid of 256 workgroups, 64 take two
+    (3000, 264, 5800, (256, 256), 1),    # 276 ragged tiles (not a multiple of 8), persistent grid
 ]
 
 
@@ -115,6 +118,25 @@ def test_planned_route_matches_oracle_and_repeats_bitwise(g, lib, cus, cuda, M, 
     y16 = g.mm_t(x, w, bias, torch.float16)
     torch.cuda.synchronize()
     assert oracle.rel_err(_np(y16), oracle.mm_t(_np(x), _np(w), _np(bias), "float16")) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("M,K,N", [(65536, 768, 768), (65536, 768, 3072), (65536, 3072, 768)])
+def test_persistent_grid_at_bert_shapes(g, cuda, M, K, N):
+    # The BERT-base linears at 256 x 256 tokens: 768 to 3072 tiles of 256x256, walked by a
+    # persistent grid of one workgroup per CU. Rows are independent, so sampled rows of the result
+    # are checked against the oracle on those rows alone; every tile is checked for repeatability.
+    x = randn((M, K), seed=5).to(cuda)
+    x[123] *= 4000.0  # a rescaled row
+    w = randn((K, N), seed=6, scale=0.02, dtype=torch.float16).to(cuda)
+    b = randn((N,), seed=7, scale=0.02).to(cuda)
+    y = g.mm_t(x, w, b, torch.float32)
+    y2 = g.mm_t(x, w, b, torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    rows = np.sort(np.random.default_rng(M + N).choice(M, 384, replace=False))
+    rows = np.unique(np.concatenate([rows, [0, 123, 255, 256, M - 1]]))
+    ref = oracle.mm_t(_np(x)[rows], _np(w), _np(b), "float32")
+    assert oracle.rel_err(_np(y)[rows], ref) <= GEMM_TOL
 
 
 CASES16 = ("skinny_m3", "skinny_m8", "gemm_m12", "gemm_m9", "skinny_tie16", "gemm_tie16")
