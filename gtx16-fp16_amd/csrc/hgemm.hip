@@ -364,7 +364,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     };
     auto dma = [&](int st, int k0) {
       const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
-  #pragma unroll
+#pragma unroll
       for (int d = 0; d < Cfg::DMA_PER_STEP; ++d) dma_op(st, k0, ra, rb, d);
     };
     // Inside the K loops, B's descriptor for successive steps comes from a running pointer (row-major
@@ -408,14 +408,14 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     // swz_b): b_off(j, b_k_in + r) = b_off(j, b_k_in) + r * BN * 2. One LDS address per block, offset
     // by the stage base, serves all of a step's transposing reads.
     uint32_t b_tr[TN];
-  #pragma unroll
+#pragma unroll
     for (int j = 0; j < TN; ++j) b_tr[j] = sB_lds + static_cast<uint32_t>(b_off(j, b_k_in));
 
     using AccT = std::conditional_t<Cfg::MF16, float4v, float16v>;
     AccT acc[TM][TN];
-  #pragma unroll
+#pragma unroll
     for (int i = 0; i < TM; ++i)
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
 
     // Fragments of one whole K step (BK/MK MFMA substeps), double-buffered across steps: the MFMAs
@@ -430,9 +430,9 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     half2v xmax[TM] = {}, xmin[TM] = {};
     auto track_amax = [&](int buf) {
       if constexpr (SPEC) {
-  #pragma unroll
+#pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < TM; ++i) {
             const half8 v = af[buf][ks][i];
             const half2v d0 = __builtin_shufflevector(v, v, 0, 1), d1 = __builtin_shufflevector(v, v, 2, 3);
@@ -450,9 +450,9 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     half2v fac[TM];
     auto scale_frags = [&](int buf) {
       if constexpr (SPEC) {
-  #pragma unroll
+#pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < TM; ++i)
             af[buf][ks][i] *= __builtin_shufflevector(fac[i], fac[i], 0, 1, 0, 1, 0, 1, 0, 1);
       }
@@ -480,7 +480,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       }
     };
     auto read_frags = [&](int buf, int st, int sta = -1) {
-  #pragma unroll
+#pragma unroll
       for (int f = 0; f < KS * (TM + TN); ++f) frag_op(buf, st, f, sta);
     };
     // MFMA m of a step: m = (ks * TM + i) * TN + jj, with j = jj on even i and TN - 1 - jj on odd i
@@ -512,24 +512,24 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
         for (int b = 0; b < RPW; b += RB) {
           u32x4 v[RB][CM];
           float am[RB];
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < RB; ++i) {
             const int grow = m0 + wave * RPW + b + i;
             const u32x4* xr = reinterpret_cast<const u32x4*>(xp + static_cast<size_t>(min(grow, M - 1)) * K);
             am[i] = 0.f;
-  #pragma unroll
+#pragma unroll
             for (int c = 0; c < CM; ++c) {
               const int idx = lane + c * kWave;
               v[i][c] = (grow < M && idx < nch) ? xr[idx] : u32x4{0u, 0u, 0u, 0u};
             }
           }
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < RB; ++i)
-  #pragma unroll
+#pragma unroll
             for (int c = 0; c < CM; ++c) am[i] = chunk_absmax(am[i], v[i][c], TX{});
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < RB; ++i) am[i] = wave_max(am[i]);
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < RB; ++i) {
             const int r = wave * RPW + b + i;
             int e;
@@ -538,7 +538,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
             if (lane == 0) s_scale[r] = sc;
             unsigned char* row_base = &sA[0][0] + r * (BK * 2);
             const int sw = Cfg::swz_a(r);
-  #pragma unroll
+#pragma unroll
             for (int c = 0; c < CM; ++c) {
               const int idx = lane + c * kWave;
               if (idx < nch) {
@@ -590,11 +590,11 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       constexpr int PARTS = NDMA - DMA0;
       if constexpr (RES) {
         if (nk > 0) {
-  #pragma unroll
+#pragma unroll
           for (int s = 0; s < NSTAGE; ++s) {
             const int k0 = kbeg + s * BK;
             const __amdgpu_buffer_rsrc_t ra = rsrc_a(k0), rb = rsrc_b(k0);
-  #pragma unroll
+#pragma unroll
             for (int d = DMA0; d < NDMA; ++d) dma_op(s, k0, ra, rb, d);
           }
         }
@@ -603,7 +603,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
         else cast_resident(static_cast<const _Float16*>(X));
       } else {
         if (nk > 0) {
-  #pragma unroll
+#pragma unroll
           for (int s = 0; s < NSTAGE; ++s) dma(s, kbeg + s * BK);
         }
       }
@@ -625,13 +625,13 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
         const int sta = RES ? (j + 1 < nk ? j + 1 : j) : -1;
         const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
         if constexpr (RESCALE) scale_frags(H);
-  #pragma unroll
+#pragma unroll
         for (int p = 0; p < PARTS; ++p) {
           dma_op(std_, kd, ra, rb, DMA0 + p);
           __builtin_amdgcn_sched_barrier(0);
-  #pragma unroll
+#pragma unroll
           for (int m = p * NMFMA / PARTS; m < (p + 1) * NMFMA / PARTS; ++m) mfma_op(H, m);
-  #pragma unroll
+#pragma unroll
           for (int f = p * NFRAG / PARTS; f < (p + 1) * NFRAG / PARTS; ++f) frag_op(H ^ 1, stf, f, sta);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -662,7 +662,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       constexpr int D = NSTAGE - 1;
       const int grp = wave >> 2;
       if (nk > 0) {
-  #pragma unroll
+#pragma unroll
         for (int s = 0; s < D; ++s) dma(s, kbeg + s * BK);
       }
       wait_dma_le<(D - 1) * NDMA>();  // step 0 has landed
@@ -680,20 +680,20 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
           const int kd = kbeg + (j + D) * BK;
           const __amdgpu_buffer_rsrc_t ra = rsrc_a(kd), rb = rsrc_b_next(kd);
           constexpr int PER = NFRAG / NDMA;
-  #pragma unroll
+#pragma unroll
           for (int d = 0; d < NDMA; ++d) {
-  #pragma unroll
+#pragma unroll
             for (int f = d * PER; f < (d + 1) * PER; ++f) frag_op(0, j % NSTAGE, f);
             dma_op((j + D) % NSTAGE, kd, ra, rb, d);
           }
-  #pragma unroll
+#pragma unroll
           for (int f = NDMA * PER; f < NFRAG; ++f) frag_op(0, j % NSTAGE, f);
         }
         wait_dma_le<(D - 1) * NDMA>();  // step j+1 has landed (this wavefront's part)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // step j's fragments are in registers
         phase_barrier();
         __builtin_amdgcn_sched_barrier(0);
-  #pragma unroll
+#pragma unroll
         for (int m = 0; m < NMFMA; ++m) mfma_op(0, m);
         __builtin_amdgcn_sched_barrier(0);
         phase_barrier();
@@ -712,9 +712,9 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     // ---- speculative A: recompute the tile where some |x| exceeded the threshold ----
     bool respec = false;  // acc comes from the rescaled A, with the row scales in s_scale
     auto zero_acc = [&]() {
-  #pragma unroll
+#pragma unroll
       for (int i = 0; i < TM; ++i)
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = AccT{};
     };
     // max with a NaN in either operand giving NaN
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       // the largest fp16 value not above the threshold; a NaN fails the comparison
       const float t = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(tbits)));
       bool within = true;
-  #pragma unroll
+#pragma unroll
       for (int i = 0; i < TM; ++i) {
         float a = nan_max(nan_max(static_cast<float>(xmax[i].x), static_cast<float>(xmax[i].y)),
                           nan_max(-static_cast<float>(xmin[i].x), -static_cast<float>(xmin[i].y)));
@@ -763,7 +763,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
           s_rowmax[tid] = e == kInfExp ? 0.f : ldexpf(1.f, -e);
         }
         __syncthreads();
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < TM; ++i) {
           const _Float16 f = static_cast<_Float16>(s_rowmax[wm0 + 32 * i + (lane & 31)]);
           fac[i] = half2v{f, f};
@@ -781,7 +781,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
         respec = true;
         note_miss();
         if (row_writer) {
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < TM; ++i) s_rowmax[wm0 + 32 * i + lane] = ramax[i];
         }
         __syncthreads();
@@ -830,11 +830,11 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
       if (SPEC && over) {
         // the last slice recomputes this tile: publish the rows' |max| in place of the partial tile
         if (row_writer) {
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < TM; ++i) store_coherent(rowmax_slot(z) + wm0 + 32 * i + lane, ramax[i]);
         }
       } else {
-  #pragma unroll
+#pragma unroll
         for (int s = 0; s < SLOTS; ++s) store_coherent4(slices, slot_off(z, s), piece(s));
       }
       if constexpr (SPEC) {
@@ -867,7 +867,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
           note_miss();
           row_factors();
           float4v sum[SLOTS];
-  #pragma unroll
+#pragma unroll
           for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
           for (int zz = 0; zz < ksplit; ++zz) {
             kbeg = zz * kchunk;
@@ -876,57 +876,57 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
             zero_acc();
             kloop4(std::false_type{}, std::true_type{});
             wait_dma_le<0>();
-  #pragma unroll
+#pragma unroll
             for (int s = 0; s < SLOTS; ++s) sum[s] += piece(s);
           }
-  #pragma unroll
+#pragma unroll
           for (int s = 0; s < SLOTS; ++s) set_piece(s, sum[s]);
         }
       } else if constexpr (SLOTS <= 16) {
         // ZB slices' loads in flight at a time
         constexpr int ZB = (128 / (SLOTS * 4)) < 1 ? 1 : ((128 / (SLOTS * 4)) > 8 ? 8 : (128 / (SLOTS * 4)));
         float4v sum[SLOTS];
-  #pragma unroll
+#pragma unroll
         for (int s = 0; s < SLOTS; ++s) sum[s] = float4v{0.f, 0.f, 0.f, 0.f};
         for (int z0 = 0; z0 < ksplit; z0 += ZB) {
           float4v v[ZB][SLOTS];
-  #pragma unroll
+#pragma unroll
           for (int b = 0; b < ZB; ++b)
-  #pragma unroll
+#pragma unroll
             for (int s = 0; s < SLOTS; ++s)
               v[b][s] = z0 + b < ksplit ? load_coherent4(slices, slot_off(z0 + b, s)) : float4v{0.f, 0.f, 0.f, 0.f};
-  #pragma unroll
+#pragma unroll
           for (int b = 0; b < ZB; ++b)
-  #pragma unroll
+#pragma unroll
             for (int s = 0; s < SLOTS; ++s)
               if (z0 + b < ksplit) sum[s] += v[b][s];
         }
-  #pragma unroll
+#pragma unroll
         for (int s = 0; s < SLOTS; ++s) set_piece(s, sum[s]);
       } else {
         // The 256x256 tile: its accumulators fill most of the register file, so the sums build up in
         // the accumulators themselves, kCh slots at a time, two slices' loads in flight.
         constexpr int kCh = 8;
         static_assert(SLOTS % kCh == 0, "whole chunks");
-  #pragma unroll
+#pragma unroll
         for (int c0 = 0; c0 < SLOTS; c0 += kCh) {
           float4v s[kCh];
-  #pragma unroll
+#pragma unroll
           for (int q = 0; q < kCh; ++q) s[q] = float4v{0.f, 0.f, 0.f, 0.f};
           for (int z0 = 0; z0 < ksplit; z0 += 2) {
             float4v v0[kCh], v1[kCh];
-  #pragma unroll
+#pragma unroll
             for (int q = 0; q < kCh; ++q) {
               v0[q] = load_coherent4(slices, slot_off(z0, c0 + q));
               v1[q] = z0 + 1 < ksplit ? load_coherent4(slices, slot_off(z0 + 1, c0 + q)) : float4v{0.f, 0.f, 0.f, 0.f};
             }
-  #pragma unroll
+#pragma unroll
             for (int q = 0; q < kCh; ++q) {
               s[q] += v0[q];
               if (z0 + 1 < ksplit) s[q] += v1[q];
             }
           }
-  #pragma unroll
+#pragma unroll
           for (int q = 0; q < kCh; ++q) set_piece(c0 + q, s[q]);
         }
       }
@@ -950,22 +950,22 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
     auto phys = [](int row, int col) {
       return (row ^ ((row >> 2) & 1)) * 32 + (Cfg::MF16 ? (col ^ (16 * ((row >> 3) & 1))) : col);
     };
-  #pragma unroll
+#pragma unroll
     for (int ri = 0; ri < Cfg::WTM / 32; ++ri) {
-  #pragma unroll
+#pragma unroll
       for (int rj = 0; rj < Cfg::WTN / 32; ++rj) {
         if constexpr (Cfg::MF16) {
-  #pragma unroll
+#pragma unroll
           for (int a = 0; a < 2; ++a)
-  #pragma unroll
+#pragma unroll
             for (int b = 0; b < 2; ++b)
-  #pragma unroll
+#pragma unroll
               for (int r = 0; r < 4; ++r) scr[phys(16 * a + 4 * fk + r, 16 * b + frow)] = acc[2 * ri + a][2 * rj + b][r];
         } else {
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 16; ++r) scr[phys(8 * (r >> 2) + 4 * fk + (r & 3), frow)] = acc[ri][rj][r];
         }
-  #pragma unroll
+#pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int id = lane + 64 * q;
           const int row = id >> 3, c4 = (id & 7) * 4;
