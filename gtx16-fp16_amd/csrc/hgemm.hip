@@ -259,10 +259,9 @@ __global__ __launch_bounds__(Cfg::THREADS) void hgemm_kernel(const _Float16* __r
   // slice-major mapping measured 1-3 us slower there.)
   // A grid of fewer workgroups than tiles (the unsplit 256-row tiles past one round: one workgroup
   // per CU, a multiple of 8) is persistent: workgroup b computes tiles b, b + gridDim.x, ... in
-  // turn, so each XCD still walks its own contiguous range, and a tile's epilogue stores drain
-  // while the next tile's DMA and MFMAs start (65536 x 768 x 768 on 256 CUs: 101.9 -> 94.4 us;
-  // 65536 x 768 x 3072: 371 -> 357 us), instead of each round's workgroups retiring and new ones
-  // being dispatched. A split grid always has one workgroup per tile, so its early returns below
+  // turn, so each XCD still walks its own contiguous range, and no round of workgroups retires
+  // and is dispatched again (65536 x 768 x 768 on 256 CUs: 101.9 -> 94.4 us; 65536 x 768 x 3072:
+  // 371 -> 357 us). A split grid always has one workgroup per tile, so its early returns below
   // end the workgroup's only tile.
   const int ntiles = ntm * ntn;
   for (int work = blockIdx.x; work < ntiles; work += gridDim.x) {
