@@ -13,10 +13,12 @@ for M=1 4096x4096 mm_t":
   part's working clock; the line reports that phase (``clock_settle``) and the shader clock the
   last timed step's GEMM held (``clock_mhz_last_timed_gemm``, from the kernel's own clock stamps).
 * ``roofline`` -- the GEMM kernel alone (the dominant kernel): 2*M*N*K flop per launch divided by
-  its average launch duration, from a HIP event pair around the GEMM of each of ``steps`` (rowscale,
-  GEMM) launch sequences on the stream the kernels run on, against the fp16 dense MFMA peak; next
-  to it the same kernel launched back to back (``kernel_ms_back_to_back``), which runs at a lower
-  clock (the part is power-limited), each with the shader clock read right after it.
+  its average duration in the timed steps (``kernel_ms``: the steps' HIP-event time per step minus
+  the rowscale kernel's own time, on the stream the kernels run on), against the fp16 dense MFMA
+  peak; next to it an event pair around the GEMM of each of ``steps`` (rowscale, GEMM) sequences
+  (``kernel_ms_event_pairs``) and the same kernel launched back to back
+  (``kernel_ms_back_to_back``, at a lower clock: the part is power-limited), each with the shader
+  clock its last GEMM held.
 * ``skinny_m1`` -- the second half of the metric: GB/s of the M=1 K=N=4096 skinny path, kernel
   time from HIP events around a captured HIP graph of launches that rotate over 16 distinct 32 MiB
   weight copies (512 MiB, twice the 256 MB Infinity Cache, so bytes come from HBM), against the
@@ -130,11 +132,15 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev, settle_ms: float = 0.0
     for _ in range(warmup):
         g.mm_t(x, w, None, torch.float32)
     torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    ev0.record()
     for _ in range(steps):
         g.mm_t(x, w, None, torch.float32)
+    ev1.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    step_ms_events = ev0.elapsed_time(ev1) / steps  # the same steps on the GPU's clock
     clock_after = gemm_clock_mhz(torch, lib, dev)  # the last timed step's GEMM
 
     # Kernel-level timing on the stream the kernels are launched on (torch's current stream).
@@ -152,12 +158,15 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev, settle_ms: float = 0.0
     def gemm():
         lib.g16_hgemm_packed_f32out(xp.data_ptr(), w.data_ptr(), out.data_ptr(), None, rs.data_ptr(), M, N, K, stream)
 
-    # The GEMM's time in the context of the timed steps: the same (rowscale, GEMM) launch sequence,
-    # with an event pair around each GEMM (the mean over `steps` sequences). The part is
-    # power-limited, and its clock follows the average power of the last milliseconds: the rowscale
-    # pass (HBM-bound, little MFMA power) between GEMMs lets it hold a higher clock for the GEMM than
-    # back-to-back GEMM launches get, so both figures are reported, each with the clock the last
-    # GEMM of its batch held (the kernel's own s_memtime / s_memrealtime stamps).
+    # The GEMM's time in the timed steps themselves: each step's HIP-event time minus the rowscale
+    # kernel's own time (measured below, back to back). Two other views are reported next to it:
+    # an event pair around the GEMM of each of `steps` (rowscale, GEMM) sequences, which adds the
+    # events' own packets to every GEMM (and read 1-7 % above the kernel trace's average on some
+    # boxes), and the GEMM launched back to back. The part is power-limited, and its clock follows
+    # the average power of the last milliseconds: the rowscale pass (HBM-bound, little MFMA power)
+    # between GEMMs lets it hold a higher clock for the GEMM than back-to-back GEMM launches get.
+    # Each figure comes with the clock the last GEMM of its batch held (the kernel's own s_memtime /
+    # s_memrealtime stamps).
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
     for b, c in evs:
         rowscale()
@@ -171,16 +180,19 @@ def bench_c4(torch, g, lib, steps: int, warmup: int, dev, settle_ms: float = 0.0
     gemm_b2b_ms = statistics.median(event_time_ms(gemm, steps, torch) for _ in range(3))
     clock_b2b = gemm_clock_mhz(torch, lib, dev)
     rowscale_ms = statistics.median(event_time_ms(rowscale, steps, torch) for _ in range(3))
+    gemm_in_steps_ms = step_ms_events - rowscale_ms
     tflops = flop / (wall_ms * 1e-3) / 1e12
-    gemm_tflops = flop / (gemm_ms * 1e-3) / 1e12
+    gemm_tflops = flop / (gemm_in_steps_ms * 1e-3) / 1e12
     # rowscale: reads 64 MiB fp32, writes 32 MiB fp16 + 16 KiB of scales
     rs_bytes = M * K * 4 + M * K * 2 + M * 4
     return {
         "wall_ms_per_step": wall_ms,
         "tflops": tflops,
-        "gemm_kernel_ms": gemm_ms,
+        "step_ms_events": step_ms_events,
+        "gemm_kernel_ms": gemm_in_steps_ms,
         "gemm_kernel_tflops": gemm_tflops,
-        "gemm_clock_mhz": clock_in_steps,
+        "gemm_event_pair_ms": gemm_ms,
+        "gemm_event_pair_clock_mhz": clock_in_steps,
         "gemm_b2b_ms": gemm_b2b_ms,
         "gemm_b2b_clock_mhz": clock_b2b,
         "rowscale_kernel_ms": rowscale_ms,
@@ -895,8 +907,11 @@ def main(argv=None) -> int:
             "frac": round(gemm_tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "traffic": traffic_bytes("gemm"),
             "kernel_ms": round(c4["gemm_kernel_ms"], 5),
-            "timing": "event pair around each GEMM of (rowscale, GEMM) launch sequences, as in the timed steps",
-            "clock_mhz": round(c4["gemm_clock_mhz"]),
+            "timing": "the timed steps' HIP-event time per step minus the rowscale kernel's own time: the GEMM's share of each step",
+            "clock_mhz": round(c4["clock_mhz_after_timed"]),
+            "step_ms_events": round(c4["step_ms_events"], 5),
+            "kernel_ms_event_pairs": round(c4["gemm_event_pair_ms"], 5),
+            "clock_mhz_event_pairs": round(c4["gemm_event_pair_clock_mhz"]),
             "kernel_ms_back_to_back": round(c4["gemm_b2b_ms"], 5),
             "clock_mhz_back_to_back": round(c4["gemm_b2b_clock_mhz"]),
             "measured_peak_random_operands": round(mp["mfma_tflops"], 1),
