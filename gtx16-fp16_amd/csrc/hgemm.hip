@@ -130,7 +130,7 @@ struct TileCfg {
   static constexpr int B_INSTR = B_BYTES / 1024 / WAVES;
   static_assert(A_INSTR >= 1 && B_INSTR >= 1 && A_BYTES % (1024 * WAVES) == 0 && B_BYTES % (1024 * WAVES) == 0,
                 "every wavefront issues the same number of DMA instructions");
-  static_assert(B_ROW_CHUNKS >= 16 && B_ROW_CHUNKS <= 64, "B swizzle needs >= 16 chunks per row");
+  static_assert(B_ROW_CHUNKS >= 8 && B_ROW_CHUNKS <= 64, "B swizzle needs >= 8 chunks per row");
   static constexpr int DMA_PER_STEP = A_INSTR + B_INSTR;  // per wavefront
   static_assert(NSTAGE >= 3 && (NSTAGE - 2) * DMA_PER_STEP <= 63, "vmcnt range");
   static_assert(!MF16 || A_ROW_CHUNKS == 4, "the 16x16x32 tile's A stage is the packed image");
@@ -145,14 +145,18 @@ struct TileCfg {
   //   chunk c at c ^ swz_b(k). With 128 columns (32x32 blocks), 4 * (k % 4); with 256 columns and
   //   16x16x32 blocks (k rows 0-3 and 8-11 in one half), 2 * (k % 4 + 4 * ((k / 8) % 2)), which
   //   puts the 8 rows' 32-byte pieces on 8 distinct bank ranges (4 * (k % 4) paired rows k and
-  //   k + 8: 1.7x the read time). Both forms give every k row a lane reads in one step (k, k + 4,
-  //   and k + MK on later substeps) the same swizzle.
+  //   k + 8: 1.7x the read time). With 64 columns (128-byte rows, two to a bank period),
+  //   4 * ((k / 2) % 2) + 2 * ((k / 8) % 2): rows k and k + 2 of one bank half take different
+  //   64-byte ranges, and rows k and k + 8 different 32-byte pieces within them, so the 32x32 reads
+  //   are conflict-free whichever of those row sets one LDS cycle serves. Every form gives every k
+  //   row a lane reads in one step (k, k + 4, and k + MK on later substeps) the same swizzle.
   __device__ static int swz_a(int row) {
     if constexpr (MF16) return pack_swz(row);
     else return (row / (16 / A_ROW_CHUNKS)) % A_ROW_CHUNKS;
   }
   __device__ static int swz_b(int k) {
     if constexpr (MF16) return ((k & 3) + 4 * ((k >> 3) & 1)) << 1;
+    else if constexpr (B_ROW_CHUNKS == 8) return (((k >> 1) & 1) << 2) | (((k >> 3) & 1) << 1);
     else return (k & 3) << 2;
   }
 };
@@ -165,6 +169,7 @@ using Cfg256n = TileCfg<256, 128, 32, 2, 4, 4, true>;  // the same schedule on h
 using Cfg128 = TileCfg<128, 128, 32, 2, 2, 4>;  // 64 KB: two workgroups per CU
 using Cfg64 = TileCfg<64, 128, 64, 1, 4, 4>;
 using Cfg32 = TileCfg<32, 128, 64, 1, 4, 4>;
+using Cfg64x64 = TileCfg<64, 64, 64, 2, 2, 4>;  // 64 KB: the square 4-wavefront tile
 
 // s_waitcnt vmcnt(N) with expcnt/lgkmcnt left alone: waits until at most N of this wavefront's
 // vector-memory operations (here: the DMA of younger stages) are still in flight.
@@ -998,7 +1003,7 @@ __global__ void copy_loop_clock(unsigned long long* dst) {
   dst[1] = g_loop_clock[1];
 }
 
-enum class Tile { T256, T256N, T128, T64, T32 };
+enum class Tile { T256, T256N, T128, T64, T32, T64x64 };
 
 struct Plan {
   Tile tile;
@@ -1006,6 +1011,10 @@ struct Plan {
   int ntm, ntn;
   int ks = 0;  // the split the tile was chosen with (the modelled choice below); 0: the planner's rule
 };
+
+// The 4-wavefront tiles (32x32x16 MFMA blocks, one barrier per K step): the ones the speculative
+// fp16 route runs on.
+inline bool four_wave(Tile t) { return t == Tile::T128 || t == Tile::T64 || t == Tile::T32 || t == Tile::T64x64; }
 
 struct KSplit {
   int ksplit;
@@ -1053,51 +1062,54 @@ int current_cus() {
 constexpr int kMaxK = G16_GEMM_MAX_K;
 constexpr int kMaxN = G16_GEMM_MAX_N;
 
-// Tile and split of the 4-wavefront tiles (32x128, 64x128, 128x128) for M > 64 outside the
+// Tile and split of the 4-wavefront tiles (32x128, 64x128, 64x64, 128x128) for M > 64 outside the
 // 256-row tiles' range: the pair with the least modelled time among those whose grid fits one round
 // on the CUs (1 to 8 slices of >= 256 K). Per tile, time (us) = a + b * KB + c * T + [split] * (d
 // + e * P + f * g / CUs + h * [tiles % 8 != 0] * T), where KB = the A and B bytes one workgroup
-// streams, (BM + 128) * kchunk * 2 / 1024; g = workgroups (tiles x slices); T = g * KB / 1024, the
+// streams, (BM + BN) * kchunk * 2 / 1024; g = workgroups (tiles x slices); T = g * KB / 1024, the
 // grid's traffic; P = the KB of fp32 partial tiles the last slice reads back; and the h term is the
 // traffic of a split grid without the XCD-grouped tile order (which split grids get only when the
 // tile count is a multiple of 8). Least-squares fit of graph-timed kernels on 256 CUs: 148
-// shapes, M = 72..1024, K = 264..14336, N = 264..14336, every tile and split that fits one round.
-// Fitted on one half of the shapes, its picks on the other half took 1.1 % more time than the best
-// measured pairs (40 random halvings; at most 1.7 %). The rule it replaces (the 32- and
-// 64-row tiles only for K <= 3072) took 7.8 % more over the same shapes and up to 2x on some, e.g.
-// 192 x 4096 x 512: 18.0 us on 128x128 tiles split 4 ways against 9.4 on 32x128 split 8 ways;
-// 96 x 14336 x 1024: 27.4 vs 15.1; 128 x 4096^2: 20.2 vs 15.8 on 64x128 split 4 ways.
+// shapes, M = 72..1024, K = 264..14336, N = 264..14336, every tile and split that fits one round
+// (133 of them have such a grid). Fitted on one half of the shapes, its picks on the other half took
+// 0.6 % more time than the best measured pairs (40 random halvings; at most 0.9 %); without the
+// 64x64 tile the best pairs themselves take 2.5 % more, and a model of the other three tiles 3.4 %.
+// Earlier rules took 7.8 % more (the 32- and 64-row tiles only for K <= 3072) and up to 2x on some
+// shapes, e.g. 192 x 4096 x 512: 18.0 us on 128x128 tiles split 4 ways against 9.4 on 32x128 split
+// 8 ways; the 64x64 tile: 160 x 1536 x 11008 (M x K x N) 17.9 -> 12.9 us against 64x128 tiles
+// split 7 ways; 1024^3 unsplit 9.4 -> 8.2 (modelled) against 32x128.
 struct TileCost {
   Tile tile;
-  int bm;
+  int bm, bn;
   double a, b, c, d, e, f, h;
 };
-constexpr TileCost kTileCost[3] = {
-    {Tile::T32, 32, 4.6481, 0.011181, 0.013789, 0.36365, 0.013646, 0.97333, 0.044944},
-    {Tile::T64, 64, 6.0134, 0.010972, 0.01919, -0.068908, 0.012927, 1.9405, 0.040133},
-    {Tile::T128, 128, 6.7721, 0.012987, 0.019247, 0.29649, 0.01301, 3.4194, 0.014194},
+constexpr TileCost kTileCost[4] = {
+    {Tile::T32, 32, 128, 4.7228, 0.011409, 0.013021, 0.43629, 0.014723, 1.0901, 0.0461},
+    {Tile::T64, 64, 128, 6.1113, 0.010968, 0.018242, 0.34527, 0.013473, 1.7771, 0.041805},
+    {Tile::T64x64, 64, 64, 4.3348, 0.013265, 0.0075242, 1.953, 0.004034, 0.88764, 0.031736},
+    {Tile::T128, 128, 128, 6.9887, 0.013018, 0.018167, 0.56691, 0.013465, 3.1856, 0.015702},
 };
 
 bool modelled_tile(int M, int N, int K, int num_cus, Plan& out) {
   double best = 0.0;
   bool found = false;
   for (const TileCost& c : kTileCost) {
-    const long tiles = static_cast<long>(ceil_div(M, c.bm)) * ceil_div(N, 128);
+    const long tiles = static_cast<long>(ceil_div(M, c.bm)) * ceil_div(N, c.bn);
     for (int want = 1; want <= 8; ++want) {
       if (want > 1 && K / want < 256) break;
       const KSplit sp = ksplit_for(K, want);
       if (sp.ksplit != want) continue;  // fewer slices than asked: counted at that count
       const long g = tiles * sp.ksplit;
       if (g > num_cus) break;
-      const double kb = (c.bm + 128) * static_cast<double>(sp.kchunk) * 2.0 / 1024.0;
+      const double kb = (c.bm + c.bn) * static_cast<double>(sp.kchunk) * 2.0 / 1024.0;
       const double traffic = static_cast<double>(g) * kb / 1024.0;
-      const double part = sp.ksplit * c.bm * 128 * 4 / 1024.0;
+      const double part = sp.ksplit * c.bm * c.bn * 4 / 1024.0;
       double t = c.a + c.b * kb + c.c * traffic;
       if (sp.ksplit > 1)
         t += c.d + c.e * part + c.f * static_cast<double>(g) / num_cus + (tiles % 8 != 0 ? c.h * traffic : 0.0);
       if (!found || t < best) {
         best = t;
-        out = Plan{c.tile, c.bm, 128, ceil_div(M, c.bm), ceil_div(N, 128), sp.ksplit};
+        out = Plan{c.tile, c.bm, c.bn, ceil_div(M, c.bm), ceil_div(N, c.bn), sp.ksplit};
         found = true;
       }
     }
@@ -1169,12 +1181,14 @@ GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b, bool re
       switch (t) {
         case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, true, false, false, false, true>;
         case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, true, false, false, false, true>;
+        case Tile::T64x64: return hgemm_kernel<Cfg64x64, OUT_F16, true, false, false, false, true>;
         default: return hgemm_kernel<Cfg32, OUT_F16, true, false, false, false, true>;
       }
     }
     switch (t) {
       case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, false, false, false, false, true>;
       case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, false, false, false, false, true>;
+      case Tile::T64x64: return hgemm_kernel<Cfg64x64, OUT_F16, false, false, false, false, true>;
       default: return hgemm_kernel<Cfg32, OUT_F16, false, false, false, false, true>;
     }
   }
@@ -1188,6 +1202,7 @@ GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b, bool re
       case Tile::T256N: return hgemm_kernel<Cfg256n, OUT_F16, true>;
       case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, true>;
       case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, true>;
+      case Tile::T64x64: return hgemm_kernel<Cfg64x64, OUT_F16, true>;
       default: return hgemm_kernel<Cfg32, OUT_F16, true>;
     }
   }
@@ -1196,6 +1211,7 @@ GemmFn<OUT_F16> gemm_fn(Tile t, bool splitk, bool packed, bool packed_b, bool re
     case Tile::T256N: return hgemm_kernel<Cfg256n, OUT_F16, false>;
     case Tile::T128: return hgemm_kernel<Cfg128, OUT_F16, false>;
     case Tile::T64: return hgemm_kernel<Cfg64, OUT_F16, false>;
+    case Tile::T64x64: return hgemm_kernel<Cfg64x64, OUT_F16, false>;
     default: return hgemm_kernel<Cfg32, OUT_F16, false>;
   }
 }
@@ -1262,7 +1278,7 @@ int gemm_launch(const uint16_t* A, const uint16_t* B, void* C, bool out_f16, con
   Plan p = choose_tile(M, N, K, num_cus);
   if (rc != nullptr && !resident_route(p, ks.ksplit, K)) return G16_E_SHAPE;
   const bool spec = sp != nullptr;
-  if (spec && ((p.tile != Tile::T128 && p.tile != Tile::T64 && p.tile != Tile::T32) || packed ||
+  if (spec && (!four_wave(p.tile) || packed ||
                ks.ksplit > kSpecMaxSplit || sp->texp < kSpecMinTexp))
     return G16_E_SHAPE;
   if (packed) {
@@ -1367,6 +1383,16 @@ extern "C" int g16_hgemm_use_packed(int M, int N, int K, int num_cus) {
   return (t == g16::Tile::T256 || t == g16::Tile::T256N) && g16_hgemm_plan(M, N, K, num_cus) == 1 ? 1 : 0;
 }
 
+extern "C" int g16_hgemm_tile(int M, int N, int K, int num_cus, int* rows, int* cols) {
+  // the tile choose_tile() plans: the one the launches, g16_hgemm_plan and the size queries use
+  if (rows == nullptr || cols == nullptr) return G16_E_NULL;
+  if (M <= 0 || N <= 0 || K <= 0) return G16_E_SHAPE;
+  const g16::Plan p = g16::choose_tile(M, N, K, num_cus > 0 ? num_cus : g16::current_cus());
+  *rows = p.bm;
+  *cols = p.bn;
+  return G16_OK;
+}
+
 extern "C" int g16_hgemm_use_packed_b(int M, int N, int K, int num_cus) {
   // A prepacked weight (g16_pack_weight) holds the B stage images of both 256-row tiles (whole
   // blocks for 256 columns, half blocks for 128), so it serves the whole packed route.
@@ -1462,7 +1488,7 @@ SpecHistory* spec_history(hipStream_t stream) {
 bool mm_t_speculative(int M, int N, int K, int num_cus) {
   if (M <= 0 || N <= 0 || K <= 0 || num_cus <= 0 || g16_hgemm_use_packed(M, N, K, num_cus) == 1) return false;
   const Tile t = choose_tile(M, N, K, num_cus).tile;
-  return t == Tile::T128 || t == Tile::T64 || t == Tile::T32;
+  return four_wave(t);
 }
 
 }  // namespace

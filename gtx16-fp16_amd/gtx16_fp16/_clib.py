@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before libg16.so)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libg16.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -50,6 +50,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_hgemm_splitk_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "g16_hgemm_splitk_counter_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "g16_hgemm_plan": (_I, [_I, _I, _I, _I]),
+    "g16_hgemm_tile": (_I, [_I, _I, _I, _I, _P, _P]),
     "g16_skinny_f32in": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P, _SZ, _P]),
     "g16_skinny_f16in": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P, _SZ, _P]),
     "g16_skinny_workspace_bytes": (_SZ, [_I, _I, _I, _I]),

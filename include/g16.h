@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 14
+#define G16_ABI_VERSION 15
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -126,11 +126,11 @@ int g16_hgemm_use_packed(int M, int N, int K, int num_cus);
  * ksplit = g16_hgemm_plan() when that is > 1, else the plain GEMM. The same result bits as the
  * separate entry points (rowscale, then GEMM); one call instead of two on a path whose small
  * shapes are bound by host and launch time. No counterpart kernel in the reference.
- *   One launch for fp16 x where the plan is a 4-wavefront tile (32x128, 64x128 or 128x128, split
- *   or not) and thresh >= 2^-8: the GEMM streams x itself as A, since a row within the threshold
- *   is its own cast, and computes a tile again, with A rescaled in registers by the rows' exponents,
- *   only where some |x| of it exceeds the threshold or is NaN (split tiles: the last slice to
- *   arrive recomputes every slice). Same result bits; no scratch is used. A weight whose call had
+ *   One launch for fp16 x where the plan is a 4-wavefront tile (32x128, 64x128, 64x64 or
+ *   128x128, split or not) and thresh >= 2^-8: the GEMM streams x itself as A, since a row within
+ *   the threshold is its own cast, and computes a tile again, with A rescaled in registers by the
+ *   rows' exponents, only where some |x| of it exceeds the threshold or is NaN (split tiles: the
+ *   last slice to arrive recomputes every slice). Same result bits; no scratch is used. A weight whose call had
  *   a tile computed again takes the other route below for its next 63 calls when the scratch the
  *   caller passed allows it (a per-device history in pinned host memory, keyed by w_t, once
  *   g16_mm_t_spec_history has enabled it).
@@ -198,6 +198,12 @@ int g16_hgemm_splitk(const uint16_t* A, const uint16_t* B, void* C, int c_is_f16
 size_t g16_hgemm_splitk_workspace_bytes(int M, int N, int K, int ksplit, int num_cus);
 size_t g16_hgemm_splitk_counter_bytes(int M, int N, int K, int ksplit, int num_cus);
 int g16_hgemm_plan(int M, int N, int K, int num_cus);
+/* The tile the GEMM entry points run (M, N, K) on for num_cus compute units (<= 0: the current
+ * device's): *rows x *cols is 32x128, 64x128, 64x64 or 128x128 (4 wavefronts), 256x128 or 256x256
+ * (8 wavefronts; the tile-packed route). The plan above and the split-buffer sizes are for this
+ * tile. No counterpart in the reference (its GEMM has one 128x128 tile); for tests and
+ * diagnostics. Returns G16_E_SHAPE for M, N or K <= 0. */
+int g16_hgemm_tile(int M, int N, int K, int num_cus, int* rows, int* cols);
 
 /* ---------------------------------------------------------------------------------------------
  * Skinny GEMM (GEMV-like) for 1 <= M <= 8: C[M,N] = A[M,K] @ B16[K,N] + bias, fp32 math on the

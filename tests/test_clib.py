@@ -93,16 +93,16 @@ def test_gemm_size_limits_refused_before_launch(lib):
 
 
 def test_splitk_launch_checks_buffers_against_the_callers_cu_count(lib):
-    # M=300, N=264: 256 CUs take 30 tiles of 32x128 (padded 320 x 384), 10 CUs take 9 tiles of
+    # M=300, N=264: 256 CUs take 25 tiles of 64x64 (padded 320 x 320), 10 CUs take 9 tiles of
     # 128x128 (384 x 384), so the 10-CU plan needs more workspace. A launch for 10 CUs handed the
     # 256-CU workspace must be refused (it used to plan with the device's own count instead).
     A = 0x1000
     M, N, K = 300, 264, 1024
     ws256 = lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, 256)
     ws10 = lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, 10)
-    assert ws256 == 2 * 320 * 384 * 4 and ws10 == 2 * 384 * 384 * 4
+    assert ws256 == 2 * 320 * 320 * 4 and ws10 == 2 * 384 * 384 * 4
     cnt10 = lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, 10)
-    assert cnt10 == 9 * 256 and lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, 256) == 30 * 256
+    assert cnt10 == 9 * 256 and lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, 256) == 25 * 256
     assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, M, N, K, 2, 10, A, ws256, A, cnt10, None) == -4
     # counters sized for 10 CUs are too few for the 256-CU grid
     assert lib.g16_hgemm_splitk(A, A, A, 0, None, None, M, N, K, 2, 256, A, ws256, A, cnt10, None) == -4
@@ -122,16 +122,16 @@ def test_plans_and_buffer_sizes(lib):
     assert lib.g16_hgemm_plan(4096, 4096, 4096, 256) == 1           # enough tiles: no split
     assert lib.g16_hgemm_plan(64, 1024, 4096, 256) > 1              # few tiles: split K
     # measured-best splits (the modelled choice for M > 64; g16_hgemm_plan(M, N, K))
-    assert lib.g16_hgemm_plan(1024, 1024, 1024, 256) == 1            # 256 tiles of 32x128
+    assert lib.g16_hgemm_plan(1024, 1024, 1024, 256) == 1            # 256 tiles of 64x64
     assert lib.g16_hgemm_plan(1024, 1024, 2048, 256) == 1
-    assert lib.g16_hgemm_plan(512, 512, 512, 256) == 1               # 64 tiles of 32x128: a split costs more than it saves
+    assert lib.g16_hgemm_plan(512, 512, 512, 256) == 1               # 64 tiles of 64x64: a split costs more than it saves
     assert lib.g16_hgemm_plan(64, 1024, 1024, 256) == 4
     assert lib.g16_hgemm_plan(64, 1024, 4096, 256) == 8
     # tiles that leave CUs idle split as far as pays off within one workgroup per CU
     assert lib.g16_hgemm_plan(512, 4096, 4096, 256) == 1             # 256 tiles of 64x128
-    assert lib.g16_hgemm_plan(128, 4096, 4096, 256) == 4             # 64 tiles of 64x128, 4 slices
-    assert lib.g16_hgemm_plan(192, 512, 4096, 256) == 8              # 24 tiles of 32x128, 8 slices
-    assert lib.g16_hgemm_plan(384, 4096, 4096, 256) == 2             # 96 tiles of 128x128, 2 slices
+    assert lib.g16_hgemm_plan(128, 4096, 4096, 256) == 2             # 128 tiles of 64x64, 2 slices
+    assert lib.g16_hgemm_plan(192, 512, 4096, 256) == 8              # 24 tiles of 64x64, 8 slices
+    assert lib.g16_hgemm_plan(384, 4096, 4096, 256) == 1             # 192 tiles of 64x128
     assert lib.g16_hgemm_plan(768, 4096, 4096, 256) == 1             # 192 tiles of 128x128: 2 slices would overflow
     # 128 tiles of 256x256 would leave half the CUs idle: 256 tiles of 256x128 instead, packed A
     # (and a packed weight, whose blocks the 128-column tiles read by halves), no split
@@ -161,10 +161,11 @@ def test_plans_and_buffer_sizes(lib):
 def test_one_launch_route_needs_no_scratch(lib):
     # mm_t's GEMM path is one launch (the cast in LDS, no scratch) exactly where the plan is the
     # unsplit 32x128 tile and K <= 1280
-    for M, N, K in [(1024, 1024, 1024), (1000, 1000, 1000), (1024, 1024, 1280), (20, 1024, 256), (20, 1024, 512),
-                    (1000, 1024, 8)]:
+    for M, N, K in [(64, 1024, 1000), (50, 1000, 1000), (20, 32768, 1280), (20, 1024, 256), (20, 1024, 512),
+                    (33, 1024, 8)]:
         assert lib.g16_mm_t_scratch_bytes(M, N, K, 256) == 0, (M, N, K)
-    for M, N, K in [(1024, 1024, 1288), (1024, 1024, 2048), (20, 1024, 1024), (64, 1024, 1024), (4096, 4096, 4096)]:
+    for M, N, K in [(1024, 1024, 1024), (20, 32768, 1288), (1024, 1024, 2048), (20, 1024, 1024), (64, 1024, 1024),
+                    (4096, 4096, 4096)]:
         assert lib.g16_mm_t_scratch_bytes(M, N, K, 256) > 0, (M, N, K)
 
 

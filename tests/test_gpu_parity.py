@@ -14,6 +14,7 @@ import torch
 
 import oracle
 from _inputs import outlier_rows, randn
+from _plan import tile as planned_tile
 
 pytestmark = pytest.mark.gpu
 
@@ -134,8 +135,8 @@ SHAPES = [  # (M, K, N) -- reference sweep, tests/test_correctness.py:14-18
 ]
 
 
-# Medium shapes run on the 32x128 or 64x128 tile, unsplit or split, as the planner's model picks
-# them (here all within one round of the CUs); bitwise repeatable either way.
+# Medium shapes run on the 4-wavefront tiles (here 64x64 and 64x128), unsplit or split, as the
+# planner's model picks them (all within one round of the CUs); bitwise repeatable either way.
 @pytest.mark.parametrize("M,K,N", [(256, 3072, 1024), (1024, 3072, 1024), (520, 2056, 3072), (1024, 1024, 1024)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 def test_short_k_small_tiles_match_oracle(g, cuda, M, K, N, out_dtype):
@@ -213,28 +214,17 @@ def test_massive_activations(g, cuda, M, in_dtype):
     assert oracle.rel_err(_np(y), ref) <= tol
 
 
-def _tile(lib, M: int, N: int, K: int, num_cus: int) -> tuple[int, int]:
-    """(rows, columns) of the tile the library runs (M, N, K) on for num_cus CUs, from its
-    split-buffer sizes for a 2-way split (one 256-byte counter line per tile, 2 x tile x 4 bytes of
-    partials per tile)."""
-    Kq = max(K, 128)
-    ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
-    area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
-    bn = 256 if area == 256 * 256 else 128
-    return area // bn, bn
-
-
 # (M, K, N, num_cus, tile): the launch plans its tile for the CU count it is given, so a small count
 # forces the larger tiles onto shapes the device's own count would give smaller ones
 SPLIT_CASES = [(64, 1024, 1024, 256, (32, 128)), (64, 4096, 1024, 256, (32, 128)),
-               (1024, 1024, 1024, 256, (32, 128)), (33, 4096, 768, 256, (32, 128)),
+               (1024, 1024, 1024, 256, (64, 64)), (33, 4096, 768, 256, (32, 128)),
                (64, 1024, 1024, 16, (64, 128)), (300, 1024, 264, 8, (128, 128)),
                (1024, 1024, 8192, 256, (256, 128)), (1024, 1024, 8192, 128, (256, 256))]
 
 
 @pytest.mark.parametrize("M,K,N,num_cus,tile", SPLIT_CASES)
 def test_splitk_deterministic_and_matches_plain(lib, cuda, M, K, N, num_cus, tile):
-    assert _tile(lib, M, N, K, num_cus) == tile
+    assert planned_tile(lib, M, N, K, num_cus) == tile
     a = randn((M, K), seed=0, dtype=torch.float16).to(cuda)
     b = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)
     bias = randn((N,), seed=2, scale=0.02).to(cuda)
@@ -293,7 +283,7 @@ def test_small_tiles_odd_and_even_step_counts(lib, cuda, M, N, bk, num_cus, tile
     # and ragged last steps, unsplit and in two slices (each slice has its own step count).
     st = _stream(cuda)
     for K in (bk * steps, bk * steps - 8):
-        assert _tile(lib, M, N, K, num_cus) == tile
+        assert planned_tile(lib, M, N, K, num_cus) == tile
         a = randn((M, K), seed=steps, dtype=torch.float16).to(cuda)
         b = randn((K, N), seed=steps + 1, scale=0.05, dtype=torch.float16).to(cuda)
         bias = randn((N,), seed=2, scale=0.02).to(cuda)

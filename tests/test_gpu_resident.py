@@ -76,13 +76,13 @@ def _two_launches(lib, x, w, bias, out16):
 
 # (M, K, N, x dtype, fp16 out, bias, special values)
 CASES = [
-    (1024, 1024, 1024, torch.float16, True, False, False),   # C1
-    (1000, 1000, 1000, torch.float32, False, True, True),    # ragged M, N, K tail; inf / NaN rows
-    (1024, 1280, 1024, torch.float32, False, False, False),  # 20 resident K steps, the most
+    (64, 1000, 1024, torch.float16, True, False, False),     # two tile rows, ragged K
+    (50, 1000, 1000, torch.float32, False, True, True),      # ragged M, N, K tail; inf / NaN rows
+    (20, 1280, 32768, torch.float32, False, False, False),   # 20 resident K steps, the most
     (20, 256, 1024, torch.float16, True, True, False),       # fewer rows than one tile
-    (1000, 8, 1024, torch.float32, False, True, False),      # one K step of 8
-    (300, 1000, 2048, torch.float16, False, True, True),     # ragged M and K, fp16 specials
-    (768, 1024, 1024, torch.float32, True, True, False),
+    (33, 8, 1024, torch.float32, False, True, False),        # one K step of 8
+    (64, 1016, 2048, torch.float16, False, True, True),      # ragged K, fp16 specials
+    (64, 1000, 1024, torch.float32, True, True, False),
 ]
 
 
@@ -117,7 +117,7 @@ def test_one_launch_equals_the_two_step_sequence_bitwise(lib, cus, cuda, M, K, N
 def test_graph_replays_of_one_launch_mm_t_match_eager(cuda):
     import gtx16_fp16 as g
 
-    shapes = [(1024, 1024, 1024, torch.float16), (1000, 1000, 1000, torch.float32), (20, 256, 1024, torch.float32)]
+    shapes = [(64, 1000, 1024, torch.float16), (50, 1000, 1000, torch.float32), (20, 256, 1024, torch.float32)]
     xs = [randn((M, K), seed=20 + i).to(dt).to(cuda) for i, (M, K, N, dt) in enumerate(shapes)]
     ws = [randn((K, N), seed=30 + i, scale=0.05, dtype=torch.float16).to(cuda) for i, (M, K, N, dt) in enumerate(shapes)]
     eager = [g.mm_t(x, w, None, torch.float32) for x, w in zip(xs, ws)]

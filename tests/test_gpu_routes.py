@@ -5,13 +5,14 @@ exactly as configured.
 * C3: ``mm_t`` at 64x1024x1024 and 64x4096x1024 (fp16 A, fp32 bias and out) at the split the
   library plans for this GPU, ten calls bitwise equal (the reference's split-K is not
   deterministic, README.md:79; tests/test_correctness.py:52-59 checks repeatability).
-* Each split-K tile through ``mm_t``: the 128x128 tile split twice (512x4096x4096), the 64x128
-  tile split twice (64x4096x11008), the 128x128 tile unsplit and split with an odd number of K
-  steps and a ragged last step, and the 32x128 tile of C3. The packed-weight 256x256 and 256x128
-  tiles the planner falls back to when no 4-wavefront grid fits one round (M >= 512, long K, large
-  N) run unsplit; past 256 tiles their grid is persistent (one workgroup per CU walking several
-  tiles), here with ragged tile counts and at the BERT-base linear shapes (sampled rows). The tile
-  each case runs on is read from the library's split-buffer sizes, so a plan change that moves a
+* Each split-K tile through ``mm_t``: the 128x128 tile split twice, the 64x128 tile split twice
+  and 4 ways, the square 64x64 tile unsplit and split 2 and 3 ways, the 128x128 tile unsplit and
+  split with an odd number of K steps and a ragged last step, and the 32x128 tile of C3 and at
+  M > 64. The packed-weight 256x256 and 256x128 tiles the planner falls back to when no
+  4-wavefront grid fits one round (M >= 512, long K, large N) run unsplit; past 256 tiles their
+  grid is persistent (one workgroup per CU walking several tiles), here with ragged tile counts and
+  at the BERT-base linear shapes (sampled rows). The tile
+  each case runs on is the library's own report (g16_hgemm_tile), so a plan change that moves a
   case to another tile fails here instead of silently dropping that tile from the tests.
 * The fp16-output golden fixtures (exact rational results, tests/golden/make_golden.py).
 
@@ -28,6 +29,7 @@ import torch
 
 import oracle
 from _inputs import randn
+from _plan import tile as planned_tile
 
 pytestmark = pytest.mark.gpu
 
@@ -59,16 +61,6 @@ def _np(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().numpy()
 
 
-def _tile(lib, M: int, N: int, K: int, num_cus: int) -> tuple[int, int]:
-    """(rows, columns) of the tile the library runs (M, N, K) on, from its split-buffer sizes for
-    a 2-way split: one 256-byte counter line per tile, 2 x tile x 4 bytes of partials per tile."""
-    Kq = max(K, 128)
-    ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
-    area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
-    bn = 256 if area == 256 * 256 else 128
-    return area // bn, bn
-
-
 def test_c1_matmul_exactly_as_configured(g, cuda):
     a = randn((1024, 1024), seed=0, dtype=torch.float16)
     b = randn((1024, 1024), seed=1, dtype=torch.float16)
@@ -86,10 +78,13 @@ def test_c1_matmul_exactly_as_configured(g, cuda):
 ROUTES = [
     (64, 1024, 1024, (32, 128), 4),      # C3
     (64, 4096, 1024, (32, 128), 8),      # C3
-    (384, 4096, 4096, (128, 128), 2),    # 128x128 split twice
+    (1024, 1024, 1024, (64, 64), 1),     # C1's shape: the square tile, unsplit
+    (100, 2048, 3072, (64, 64), 2),      # the square tile split twice, ragged M
+    (320, 4056, 1024, (64, 64), 3),      # ... 3 ways: slices of 22, 22 and 20 K steps, the last ragged
+    (320, 8192, 4096, (128, 128), 2),    # 128x128 split twice
     (64, 4096, 11008, (64, 128), 2),     # 64x128 split twice
-    (128, 4096, 4096, (64, 128), 4),     # 64x128 split 4 ways at M > 64
-    (192, 4096, 512, (32, 128), 8),      # 32x128 split 8 ways at M > 64
+    (128, 8192, 4096, (64, 128), 4),     # 64x128 split 4 ways at M > 64
+    (256, 8192, 264, (32, 128), 8),      # 32x128 split 8 ways at M > 64
     (768, 4056, 4096, (128, 128), 1),    # 128x128 unsplit: 127 K steps, the last one ragged
     (384, 4056, 3072, (128, 128), 3),    # split: slices of 44, 44 and 39 K steps, the last one ragged
     (768, 4096, 11008, (256, 256), 1),   # no 4-wavefront grid fits one round: packed 256x256 tiles
@@ -103,7 +98,7 @@ ROUTES = [
 def test_planned_route_matches_oracle_and_repeats_bitwise(g, lib, cus, cuda, M, K, N, tile, ks):
     if cus != 256:
         pytest.skip(f"the route table is for 256 CUs (this device has {cus})")
-    assert _tile(lib, M, N, K, cus) == tile
+    assert planned_tile(lib, M, N, K, cus) == tile
     assert lib.g16_hgemm_plan(M, N, K, cus) == ks
     x = randn((M, K), seed=0, dtype=torch.float16).to(cuda)
     w = randn((K, N), seed=1, scale=0.02, dtype=torch.float16).to(cuda)

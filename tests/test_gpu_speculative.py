@@ -1,5 +1,5 @@
-"""One-launch small GEMMs for fp16 activations: on the 4-wavefront tiles (32x128, 64x128, 128x128,
-split or not), g16_mm_t_gemm streams x itself as A. A row whose |max| is within the threshold has
+"""One-launch small GEMMs for fp16 activations: on the 4-wavefront tiles (32x128, 64x128, 64x64,
+128x128, split or not), g16_mm_t_gemm streams x itself as A. A row whose |max| is within the threshold has
 scale 1, so its rowscale cast is x and the result is exactly the cast path's; where some |x| of a
 tile exceeds the threshold (or is NaN), that tile is computed again with its A fragments rescaled in
 registers, by the rows' exponents taken from the maxima the first pass tracked (by the
@@ -21,6 +21,7 @@ import torch
 
 import oracle
 from _inputs import outlier_rows, randn
+from _plan import tile as planned_tile
 
 pytestmark = pytest.mark.gpu
 
@@ -39,11 +40,6 @@ def cus(cuda):
     return torch.cuda.get_device_properties(cuda).multi_processor_count
 
 
-def _tile(lib, M, N, K, num_cus):
-    Kq = max(K, 128)
-    ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
-    area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
-    return area // 128
 
 
 def _bufs(lib, M, N, K, num_cus, dev):
@@ -117,30 +113,33 @@ def _inputs(M, K, N, kind: str, seed: int, out16: bool):
     return x.to(torch.float16), randn((K, N), seed=seed + 1, scale=0.05, dtype=torch.float16)
 
 
-# (M, K, N, tile rows on 256 CUs, planned split on 256 CUs)
+# (M, K, N, tile on 256 CUs, planned split on 256 CUs)
 ROUTES = [
-    (1024, 1024, 1024, 32, 1),    # C1: resident route (a recomputed tile casts into LDS)
-    (64, 1024, 1024, 32, 4),      # C3
-    (64, 4096, 1024, 32, 8),      # C3
-    (1024, 2048, 1024, 32, 1),    # unsplit 32x128 past the resident K: recomputes from the scratch
-    (100, 1000, 264, 32, 3),      # ragged M, N, K
-    (64, 4096, 11008, 64, 2),     # 64x128 split twice
-    (128, 4096, 4096, 64, 4),     # 64x128 split 4 ways
-    (192, 4096, 512, 32, 8),      # 32x128 split 8 ways at M > 64
-    (384, 4096, 4096, 128, 2),    # 128x128 split twice
-    (384, 4056, 3072, 128, 3),    # 128x128 split 3 ways, ragged last K step
-    (768, 4056, 4096, 128, 1),    # 128x128 unsplit, ragged K tail
-    (40, 8, 136, 32, 1),          # one K step of 8
+    (1024, 1024, 1024, (64, 64), 1),     # C1: the square tile, unsplit
+    (64, 1024, 1024, (32, 128), 4),      # C3
+    (64, 4096, 1024, (32, 128), 8),      # C3
+    (1000, 1000, 1000, (64, 64), 1),     # ragged M, N, K on the square tile
+    (100, 2048, 3072, (64, 64), 2),      # the square tile split twice, ragged M
+    (320, 4056, 1024, (64, 64), 3),      # ... 3 ways, ragged last K step
+    (72, 3072, 264, (64, 64), 8),        # ... 8 ways, ragged M and N
+    (100, 1000, 264, (32, 128), 3),      # ragged M, N, K
+    (64, 4096, 11008, (64, 128), 2),     # 64x128 split twice
+    (128, 8192, 4096, (64, 128), 4),     # 64x128 split 4 ways at M > 64
+    (256, 8192, 264, (32, 128), 8),      # 32x128 split 8 ways at M > 64
+    (320, 8192, 4096, (128, 128), 2),    # 128x128 split twice
+    (384, 4056, 3072, (128, 128), 3),    # 128x128 split 3 ways, ragged last K step
+    (768, 4056, 4096, (128, 128), 1),    # 128x128 unsplit, ragged K tail
+    (40, 8, 136, (32, 128), 1),          # one K step of 8
 ]
 KINDS = ["within", "over", "edge", "special", "nan_over"]
 
 
-@pytest.mark.parametrize("M,K,N,bm,ks", ROUTES)
+@pytest.mark.parametrize("M,K,N,tile,ks", ROUTES)
 @pytest.mark.parametrize("kind", KINDS)
-def test_one_launch_equals_the_two_step_sequence_bitwise(lib, cus, cuda, M, K, N, bm, ks, kind):
+def test_one_launch_equals_the_two_step_sequence_bitwise(lib, cus, cuda, M, K, N, tile, ks, kind):
     if cus != 256:
         pytest.skip(f"the route table is for 256 CUs (this device has {cus})")
-    assert _tile(lib, M, N, K, cus) == bm
+    assert planned_tile(lib, M, N, K, cus) == tile
     assert lib.g16_hgemm_plan(M, N, K, cus) == ks
     out16 = (M + K) % 2 == 0
     use_bias = (N // 8) % 2 == 1
@@ -223,11 +222,11 @@ def test_thresholds_below_two_to_minus_8_take_the_two_launch_route(lib, cus, cud
     assert torch.equal(out.view(torch.int32), two.view(torch.int32))
 
 
-@pytest.mark.parametrize("M,K,N,with_scratch", [(64, 4096, 1024, True), (1024, 1024, 1024, False)])
+@pytest.mark.parametrize("M,K,N,with_scratch", [(64, 4096, 1024, True), (64, 1000, 1024, False)])
 def test_a_recomputed_weight_takes_the_other_route_for_63_calls(lib, cus, cuda, M, K, N, with_scratch):
     """After a call whose tile was computed again, the weight's next 63 calls take the other route
     -- the two-launch one where the caller passed the scratch it needs (64x4096x1024), the resident
-    one-launch cast into LDS where the plan allows it (1024^3, no scratch) -- then speculation
+    one-launch cast into LDS where the plan allows it (64x1000x1024, no scratch) -- then speculation
     resumes; every call's result is the two-step sequence's, bit for bit."""
     xo, w = _inputs(M, K, N, "over", seed=11, out16=False)
     xw, _ = _inputs(M, K, N, "within", seed=12, out16=False)

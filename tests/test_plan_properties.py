@@ -11,6 +11,7 @@ hypothesis = pytest.importorskip("hypothesis")
 from hypothesis import given, settings, strategies as st  # noqa: E402
 
 from gtx16_fp16 import _clib  # noqa: E402
+from _plan import tile as planned_tile  # noqa: E402
 
 
 @pytest.fixture(scope="module")
@@ -23,21 +24,21 @@ def _ceil(a: int, b: int) -> int:
 
 
 # The GEMM tiles the library has kernels for, by (rows, columns).
-TILES = {(32, 128), (64, 128), (128, 128), (256, 128), (256, 256)}
+TILES = {(32, 128), (64, 128), (64, 64), (128, 128), (256, 128), (256, 256)}
 
 
 def _tile(lib, M: int, N: int, K: int, num_cus: int) -> tuple[int, int, int]:
-    """(rows, columns, count) of the tile the library runs this shape on for num_cus CUs, read
-    from the library's own size queries for a 2-way split (the tile does not depend on the split):
-    the counters hold one 256-byte line per tile and the partials 2 slices x tile x 4 bytes. (Split
-    slices start on multiples of 64 K, so K < 128 cannot split; those shapes are asked about at
-    K = 128, which plans the same tile: below 512 K nothing splits, and the smallest 4-wavefront
-    tile whose grid fits one round wins.)"""
-    Kq = max(K, 128)
-    ntiles = lib.g16_hgemm_splitk_counter_bytes(M, N, Kq, 2, num_cus) // 256
-    area = lib.g16_hgemm_splitk_workspace_bytes(M, N, Kq, 2, num_cus) // (2 * 4 * ntiles)
-    bn = 256 if area == 256 * 256 else 128
-    return area // bn, bn, ntiles
+    """(rows, columns, count) of the tile the library plans for this shape on num_cus CUs, from
+    g16_hgemm_tile, checked against the library's own split-buffer sizes for a 2-way split (the tile
+    does not depend on the split): the counters hold one 256-byte line per tile and the partials
+    2 slices x tile x 4 bytes. (Split slices start on multiples of 64 K, so K < 128 cannot split
+    and has no split sizes to check.)"""
+    bm, bn = planned_tile(lib, M, N, K, num_cus)
+    ntiles = _ceil(M, bm) * _ceil(N, bn)
+    if K >= 128:
+        assert lib.g16_hgemm_splitk_counter_bytes(M, N, K, 2, num_cus) == ntiles * 256
+        assert lib.g16_hgemm_splitk_workspace_bytes(M, N, K, 2, num_cus) == ntiles * 2 * bm * bn * 4
+    return bm, bn, ntiles
 
 
 dims = st.integers(min_value=1, max_value=1 << 15).map(lambda v: v * 8)
@@ -60,7 +61,7 @@ def test_gemm_plan_limits(lib, M, N, K, num_cus):
     assert lib.g16_hgemm_use_packed(M, N, K, num_cus) == (1 if (bm == 256 and ks == 1) else 0)
     assert 1 <= ks <= 8
     # the 4-wavefront tiles' grid fits one round of the CUs whenever one of them can
-    if 32 < M and bm < 256 and min(_ceil(M, r) * _ceil(N, 128) for r in (32, 64, 128)) <= num_cus:
+    if 32 < M and bm < 256 and min(_ceil(M, r) * _ceil(N, c) for r, c in TILES if r < 256) <= num_cus:
         assert tiles * ks <= num_cus
     if ks > 1:
         # split only when tiles leave CUs idle, never past one workgroup per CU, >= 256 K a slice
