@@ -1072,8 +1072,8 @@ constexpr int kMaxN = G16_GEMM_MAX_N;
 // tile count is a multiple of 8). Least-squares fit of graph-timed kernels on 256 CUs: 148
 // shapes, M = 72..1024, K = 264..14336, N = 264..14336, every tile and split that fits one round
 // (133 of them have such a grid). Fitted on one half of the shapes, its picks on the other half took
-// 0.6 % more time than the best measured pairs (40 random halvings; at most 0.9 %); without the
-// 64x64 tile the best pairs themselves take 2.5 % more, and a model of the other three tiles 3.4 %.
+// 0.56 % more time than the best measured pairs (40 random halvings; at most 0.77 %); without the
+// 64x64 tile the best pairs themselves take 2.6 % more, and a model of the other three tiles 3.6 %.
 // Earlier rules took 7.8 % more (the 32- and 64-row tiles only for K <= 3072) and up to 2x on some
 // shapes, e.g. 192 x 4096 x 512: 18.0 us on 128x128 tiles split 4 ways against 9.4 on 32x128 split
 // 8 ways; the 64x64 tile: 160 x 1536 x 11008 (M x K x N) 17.9 -> 12.9 us against 64x128 tiles
@@ -1084,10 +1084,10 @@ struct TileCost {
   double a, b, c, d, e, f, h;
 };
 constexpr TileCost kTileCost[4] = {
-    {Tile::T32, 32, 128, 4.7228, 0.011409, 0.013021, 0.43629, 0.014723, 1.0901, 0.0461},
-    {Tile::T64, 64, 128, 6.1113, 0.010968, 0.018242, 0.34527, 0.013473, 1.7771, 0.041805},
-    {Tile::T64x64, 64, 64, 4.3348, 0.013265, 0.0075242, 1.953, 0.004034, 0.88764, 0.031736},
-    {Tile::T128, 128, 128, 6.9887, 0.013018, 0.018167, 0.56691, 0.013465, 3.1856, 0.015702},
+    {Tile::T32, 32, 128, 4.8257, 0.011467, 0.012217, 0.35769, 0.01376, 1.218, 0.046066},
+    {Tile::T64, 64, 128, 6.1411, 0.011029, 0.016788, 0.31265, 0.012935, 2.0704, 0.042793},
+    {Tile::T64x64, 64, 64, 4.4223, 0.013086, 0.0069148, 1.8756, 0.0031762, 0.98682, 0.03103},
+    {Tile::T128, 128, 128, 7.2055, 0.013027, 0.01719, 0.43912, 0.013514, 2.9942, 0.016906},
 };
 
 bool modelled_tile(int M, int N, int K, int num_cus, Plan& out) {

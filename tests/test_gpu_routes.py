@@ -84,7 +84,7 @@ ROUTES = [
     (320, 8192, 4096, (128, 128), 2),    # 128x128 split twice
     (64, 4096, 11008, (64, 128), 2),     # 64x128 split twice
     (128, 8192, 4096, (64, 128), 4),     # 64x128 split 4 ways at M > 64
-    (256, 8192, 264, (32, 128), 8),      # 32x128 split 8 ways at M > 64
+    (256, 11008, 264, (32, 128), 8),     # 32x128 split 8 ways at M > 64
     (768, 4056, 4096, (128, 128), 1),    # 128x128 unsplit: 127 K steps, the last one ragged
     (384, 4056, 3072, (128, 128), 3),    # split: slices of 44, 44 and 39 K steps, the last one ragged
     (768, 4096, 11008, (256, 256), 1),   # no 4-wavefront grid fits one round: packed 256x256 tiles

@@ -125,7 +125,7 @@ ROUTES = [
     (100, 1000, 264, (32, 128), 3),      # ragged M, N, K
     (64, 4096, 11008, (64, 128), 2),     # 64x128 split twice
     (128, 8192, 4096, (64, 128), 4),     # 64x128 split 4 ways at M > 64
-    (256, 8192, 264, (32, 128), 8),      # 32x128 split 8 ways at M > 64
+    (256, 11008, 264, (32, 128), 8),     # 32x128 split 8 ways at M > 64
     (320, 8192, 4096, (128, 128), 2),    # 128x128 split twice
     (384, 4056, 3072, (128, 128), 3),    # 128x128 split 3 ways, ragged last K step
     (768, 4056, 4096, (128, 128), 1),    # 128x128 unsplit, ragged K tail
