@@ -93,6 +93,42 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const TX* __restrict__ X,
   if (lane == 0) S[row] = sc;
 }
 
+// Whole rows of exactly 64 * CH chunks (K = 4096 for both input types), and no padding rows:
+// every wavefront casts two rows, r and r + M / 2, and issues the second row's loads before the
+// first row's stores, with no per-chunk conditions. Same arithmetic and stores as above
+// (4096 x 4096 fp32 into the packed layout, event-timed on one box: 16.35 -> 15.75 us alone,
+// 120.85 -> 120.41 us per (cast, GEMM) pair of mm_t, medians of 8 alternating batches).
+template <typename TX, int CH, bool PACK>
+__global__ __launch_bounds__(256) void rowscale_rows2_kernel(const TX* X, _Float16* Y, float* S, int M, int K, int texp) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int nks = packed_ksteps(K);
+  const int half = M / 2;
+  const int r0 = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  auto load = [&](int row, u32x4 (&buf)[CH]) {
+    const u32x4* xr = reinterpret_cast<const u32x4*>(X + static_cast<size_t>(row) * K);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) buf[c] = xr[lane + c * kWave];
+  };
+  auto finish = [&](int row, const u32x4 (&buf)[CH]) {
+    float amax = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) amax = chunk_absmax(amax, buf[c], TX{});
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    int e;
+    float sc;
+    row_exponent(amax, texp, e, sc);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) store_scaled(out_at<TX, PACK>(Y, row, K, lane + c * kWave, nks), buf[c], e, TX{});
+    if (lane == 0) S[row] = sc;
+  };
+  u32x4 a[CH], b[CH];
+  load(r0, a);
+  load(r0 + half, b);
+  finish(r0, a);
+  finish(r0 + half, b);
+}
+
 template <typename TX, int CH, bool PACK>
 int rowscale_launch(const void* X, void* Y, float* S, int M, int K, float thresh, void* stream) {
   if (M < 0 || K < 0 || K % 8 != 0) return G16_E_SHAPE;
@@ -101,6 +137,13 @@ int rowscale_launch(const void* X, void* Y, float* S, int M, int K, float thresh
   if (!aligned16(X) || !aligned16(Y)) return G16_E_ALIGN;
   const int texp = thresh_exponent(thresh);
   if (texp == -1000) return G16_E_SHAPE;
+  constexpr int EPC = 16 / static_cast<int>(sizeof(TX));
+  if (K == kWave * CH * EPC && M % (2 * kRowsPerBlock) == 0 && (!PACK || M % kPackRows == 0)) {
+    // whole rows, an even number of workgroup row sets, no padding rows: the two-row form
+    return launch(rowscale_rows2_kernel<TX, CH, PACK>, dim3(M / (2 * kRowsPerBlock)), dim3(256),
+                  static_cast<hipStream_t>(stream), static_cast<const TX*>(X), static_cast<_Float16*>(Y), S, M, K,
+                  texp);
+  }
   const int rows = PACK ? ceil_div(M, kPackRows) * kPackRows : M;
   const dim3 grid(ceil_div(rows, kRowsPerBlock)), block(256);
   return launch(rowscale_kernel<TX, CH, PACK>, grid, block, static_cast<hipStream_t>(stream),

@@ -70,8 +70,10 @@ KAT_AMAX = [0.0, 1.0, 1023.9999, 1024.0, float(np.nextafter(np.float32(1024), np
 
 
 @pytest.mark.parametrize("K", [8, 136, 1032, 3072, 4096, 8200])
-def test_rowscale_f32_bitexact(lib, cuda, K):
-    M = len(KAT_AMAX) + 20
+@pytest.mark.parametrize("extra", [20, 21])
+def test_rowscale_f32_bitexact(lib, cuda, K, extra):
+    # 31 or 32 rows: at K = 4096 with a multiple of 8 rows the cast takes its two-row form
+    M = len(KAT_AMAX) + extra
     x = randn((M, K), seed=K)
     for i, a in enumerate(KAT_AMAX):  # row i has |max| exactly a (at a column that depends on i)
         x[i] = x[i].clamp(-0.5, 0.5)
@@ -446,7 +448,7 @@ def _rowscale_pack_gpu(lib, x: torch.Tensor):
     return yp, s
 
 
-@pytest.mark.parametrize("M,K", [(1, 8), (255, 136), (300, 4096), (512, 40)])
+@pytest.mark.parametrize("M,K", [(1, 8), (255, 136), (300, 4096), (512, 40), (512, 4096)])
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.float16])
 def test_rowscale_pack_bitexact(lib, cuda, M, K, in_dtype):
     from _packing import pack_a
