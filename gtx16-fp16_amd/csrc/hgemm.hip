@@ -8,10 +8,11 @@
 //
 // Structure:
 //   * A workgroup owns a BM x BN output tile; each wavefront owns a (BM/WGM) x (BN/WGN) sub-tile
-//     made of MFMA blocks with fp32 accumulators. The large tile is 256x256 with 8 wavefronts (two
-//     per SIMD) on 16x16 blocks of v_mfma_f32_16x16x32_f16; smaller tiles (128x128, 64x128,
-//     32x128) use 4 wavefronts on 32x32 blocks of v_mfma_f32_32x32x16_f16 and serve small M and
-//     split-K. Both instructions have the same peak rate; on random operands the 16x16x32 one
+//     made of MFMA blocks with fp32 accumulators. The large tiles are 256x256 and 256x128 with 8
+//     wavefronts (two per SIMD) on 16x16 blocks of v_mfma_f32_16x16x32_f16; smaller tiles
+//     (128x128, 64x128, 64x64, 32x128) use 4 wavefronts on 32x32 blocks of
+//     v_mfma_f32_32x32x16_f16 and serve small and medium M and split-K. Both instructions have the
+//     same peak rate; on random operands the 16x16x32 one
 //     draws less power, and at 4096^3 the part is power-limited (it holds ~1.6 GHz, not 2.4), so
 //     the large tile runs 4-6 % faster with it.
 //   * K advances in steps of BK through a ring of NSTAGE LDS stages filled by DMA
@@ -36,6 +37,8 @@
 //     (and, for unsplit grids of any other count, to the same contiguous runs of T / 8 or T / 8 + 1
 //     tiles per XCD), giving each XCD a contiguous run of tiles, which a grouped (GROUP_M rows at a
 //     time) order turns into a compact 2-D block that shares A rows and B columns in that XCD's L2.
+//     An unsplit 256-row grid with more tiles than CUs is persistent: one workgroup per CU (a
+//     multiple of 8) walks tiles b, b + G, b + 2G, ... of the same sequence.
 //   * Resident A (the unsplit 32x128 tile with K <= kResidentSteps * 64, mm_t's GEMM path in one
 //     launch): the workgroup reads its 32 rows of the fp32/fp16 activations itself, computes each
 //     row's scale (rowscale_math.hpp, the rowscale kernel's arithmetic) and writes the scaled fp16

@@ -273,9 +273,10 @@ def test_splitk_fp16_output(lib, cuda):
     assert oracle.rel_err(_np(c.float()), ref) <= GEMM_TOL
 
 
-# (M, N, K step, num_cus, tile): the 128x128 (BK 32), 64x128 and 32x128 (BK 64) tiles, each forced by
-# the CU count the launch is planned for
-SMALL_TILES = [(300, 264, 32, 8, (128, 128)), (64, 1024, 64, 12, (64, 128)), (20, 200, 64, 256, (32, 128))]
+# (M, N, K step, num_cus, tile): the 128x128 (BK 32), 64x128, 64x64 and 32x128 (BK 64) tiles, each
+# forced by the CU count the launch is planned for (the 64x64 case with ragged M and N)
+SMALL_TILES = [(300, 264, 32, 8, (128, 128)), (64, 1024, 64, 12, (64, 128)), (100, 200, 64, 16, (64, 64)),
+               (20, 200, 64, 256, (32, 128))]
 
 
 @pytest.mark.parametrize("M,N,bk,num_cus,tile", SMALL_TILES)
