@@ -1,10 +1,10 @@
-/* _g16fast: a CPython extension that calls the two per-call entry points of libg16.so that sit on
- * latency-bound paths -- g16_skinny_f32in (the FastLinear decode shortcut, the counterpart of the
- * reference's PreparedLaunch, src/gtx16_fp16/kernels.py:324-338) and g16_mm_t_gemm (mm_t's GEMM
- * path, ops.py:86-108) -- with METH_FASTCALL argument parsing. Through ctypes the same calls spend
+/* _g16fast: a CPython extension that calls the per-call entry points of libg16.so that sit on
+ * latency-bound paths -- g16_skinny_f32in and g16_skinny_strips_f32in (the FastLinear decode
+ * shortcut, the counterpart of the reference's PreparedLaunch, src/gtx16_fp16/kernels.py:324-338)
+ * and g16_mm_t_gemm (mm_t's GEMM path, ops.py:86-108) -- with METH_FASTCALL argument parsing. Through ctypes the same calls spend
  * ~0.1 us per argument converting them; here the conversion is a few ns per argument.
  *
- * The module does not link libg16.so: bind() receives the addresses of the two functions from the
+ * The module does not link libg16.so: bind() receives the addresses of the three functions from the
  * library the ctypes binding already loaded, so both bindings call into the same instance. Pointer
  * arguments are Python ints or None (NULL); every call returns the entry point's int status. The
  * GIL is released around the call, as ctypes does.
@@ -19,7 +19,9 @@ typedef int (*skinny_fn)(const void*, const void*, void*, const void*, int, int,
 typedef int (*mm_t_gemm_fn)(const void*, int, const void*, void*, int, const void*, float, int, int, int, int, void*,
                             size_t, void*, size_t, void*, size_t, void*);
 
+typedef int (*strips_fn)(const void*, const void*, void*, const void*, int, int, int, void*);
 static skinny_fn g_skinny_f32in = NULL;
+static strips_fn g_strips_f32in = NULL;
 static mm_t_gemm_fn g_mm_t_gemm = NULL;
 
 static int as_ptr(PyObject* o, void** out) {
@@ -55,14 +57,17 @@ static int check_nargs(const char* name, Py_ssize_t nargs, Py_ssize_t want) {
 
 static PyObject* fast_bind(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
   (void)self;
-  void *skinny, *gemm;
-  if (check_nargs("bind", nargs, 2) || as_ptr(args[0], &skinny) || as_ptr(args[1], &gemm)) return NULL;
-  if (skinny == NULL || gemm == NULL) {
-    PyErr_SetString(PyExc_ValueError, "bind() needs two non-NULL function addresses");
+  void *skinny, *gemm, *strips;
+  if (check_nargs("bind", nargs, 3) || as_ptr(args[0], &skinny) || as_ptr(args[1], &gemm) ||
+      as_ptr(args[2], &strips))
+    return NULL;
+  if (skinny == NULL || gemm == NULL || strips == NULL) {
+    PyErr_SetString(PyExc_ValueError, "bind() needs three non-NULL function addresses");
     return NULL;
   }
   g_skinny_f32in = (skinny_fn)skinny;
   g_mm_t_gemm = (mm_t_gemm_fn)gemm;
+  g_strips_f32in = (strips_fn)strips;
   Py_RETURN_NONE;
 }
 
@@ -87,6 +92,21 @@ static PyObject* fast_skinny_f32in(PyObject* self, PyObject* const* args, Py_ssi
     return NULL;
   Py_BEGIN_ALLOW_THREADS
   st = g_skinny_f32in(x, w, out, bias, M, N, K, ksplit, part, part_bytes, cnt, cnt_bytes, stream);
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(st);
+}
+
+/* skinny_strips_f32in(x, wd, out, bias, M, N, K, stream) -> status of g16_skinny_strips_f32in */
+static PyObject* fast_strips_f32in(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  (void)self;
+  void *x, *wd, *out, *bias, *stream;
+  int M, N, K, st;
+  if (check_bound((const void*)g_strips_f32in) || check_nargs("skinny_strips_f32in", nargs, 8)) return NULL;
+  if (as_ptr(args[0], &x) || as_ptr(args[1], &wd) || as_ptr(args[2], &out) || as_ptr(args[3], &bias) ||
+      as_int(args[4], &M) || as_int(args[5], &N) || as_int(args[6], &K) || as_ptr(args[7], &stream))
+    return NULL;
+  Py_BEGIN_ALLOW_THREADS
+  st = g_strips_f32in(x, wd, out, bias, M, N, K, stream);
   Py_END_ALLOW_THREADS
   return PyLong_FromLong(st);
 }
@@ -118,7 +138,10 @@ static PyObject* fast_mm_t_gemm(PyObject* self, PyObject* const* args, Py_ssize_
 }
 
 static PyMethodDef fast_methods[] = {
-    {"bind", (PyCFunction)(void (*)(void))fast_bind, METH_FASTCALL, "bind(skinny_f32in_addr, mm_t_gemm_addr)"},
+    {"bind", (PyCFunction)(void (*)(void))fast_bind, METH_FASTCALL,
+     "bind(skinny_f32in_addr, mm_t_gemm_addr, skinny_strips_f32in_addr)"},
+    {"skinny_strips_f32in", (PyCFunction)(void (*)(void))fast_strips_f32in, METH_FASTCALL,
+     "g16_skinny_strips_f32in with fast argument parsing; returns its status"},
     {"skinny_f32in", (PyCFunction)(void (*)(void))fast_skinny_f32in, METH_FASTCALL,
      "g16_skinny_f32in with fast argument parsing; returns its status"},
     {"mm_t_gemm", (PyCFunction)(void (*)(void))fast_mm_t_gemm, METH_FASTCALL,

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before libg16.so)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libg16.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -58,6 +58,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_skinny_plan": (_I, [_I, _I, _I, _I]),
     "g16_skinny_strip_cols": (_I, [_I, _I]),
     "g16_skinny_f32in_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "g16_pack_decode_weight": (_I, [_P, _P, _I, _I, _P]),
+    "g16_skinny_strips_f32in": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "g16_skinny_strips_f16in": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "g16_skinny_strips_route": (_I, [_I, _I, _I, _I]),
     "g16_gemm_clock": (_I, [_P, _P]),
     "g16_peak_flops_per_lane_iter": (ctypes.c_double, [_I]),
     "g16_peak_run": (_I, [_I, _I, _I, _P, _P]),
@@ -100,7 +104,7 @@ _fast = None
 
 def fast():
     """The CPython extension ``_g16fast`` (built next to the library from ``csrc/fastcall.c``), bound
-    to the loaded library: ``skinny_f32in`` and ``mm_t_gemm`` take the same arguments as the C
+    to the loaded library: ``skinny_f32in``, ``skinny_strips_f32in`` and ``mm_t_gemm`` take the same arguments as the C
     entry points (pointers as ints or None) and return their status, with argument conversion
     that costs a few ns per argument instead of ctypes' ~0.1 us. Missing -> ``RuntimeError``."""
     global _fast
@@ -118,7 +122,8 @@ def fast():
             mod = importlib.util.module_from_spec(spec)
             spec.loader.exec_module(mod)
             mod.bind(ctypes.cast(lib.g16_skinny_f32in, ctypes.c_void_p).value,
-                     ctypes.cast(lib.g16_mm_t_gemm, ctypes.c_void_p).value)
+                     ctypes.cast(lib.g16_mm_t_gemm, ctypes.c_void_p).value,
+                     ctypes.cast(lib.g16_skinny_strips_f32in, ctypes.c_void_p).value)
             _fast = mod
     return _fast
 

@@ -234,6 +234,49 @@ def pack_weight(w_t: torch.Tensor) -> torch.Tensor:
     return wp
 
 
+STRIPS_MAX_M = 4  # G16_STRIPS_MAX_M
+
+
+def pack_decode_weight(w_t: torch.Tensor) -> torch.Tensor:
+    """w_t [K, N] fp16 (CUDA, contiguous, K and N multiples of 8) -> its decode layout for
+    ``skinny_strips``: N/8 strips of 8 columns, each all K rows long and contiguous, as an
+    [N/8, K, 8] fp16 tensor (``wd[s, k, c] == w_t[k, 8 * s + c]``)."""
+    if not (w_t.is_cuda and w_t.dim() == 2 and w_t.dtype == torch.float16 and w_t.is_contiguous()
+            and w_t.data_ptr() % 16 == 0 and w_t.shape[0] % 8 == 0 and w_t.shape[1] % 8 == 0):
+        raise ValueError("pack_decode_weight: w_t must be a contiguous, 16-byte aligned fp16 CUDA tensor "
+                         "with both dimensions multiples of 8")
+    lib = _clib.load()
+    K, N = w_t.shape
+    wd = torch.empty(N // 8, K, 8, device=w_t.device, dtype=torch.float16)
+    _clib.check(lib.g16_pack_decode_weight(w_t.data_ptr(), wd.data_ptr(), K, N, stream_handle(w_t.device.index or 0)),
+                "decode-layout packing")
+    return wd
+
+
+def skinny_strips(x2d: torch.Tensor, wd: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """The skinny product on a weight's decode layout ``wd = pack_decode_weight(w_t)``: fp32
+    ``x2d @ w_t + bias`` for 1 <= M <= STRIPS_MAX_M rows of fp32 or fp16 activations, in fp32
+    arithmetic on the activations as given (the skinny path's semantics, one workgroup per strip of
+    8 columns over all of K)."""
+    if not (wd.is_cuda and wd.dim() == 3 and wd.shape[2] == 8 and wd.dtype == torch.float16 and wd.is_contiguous()):
+        raise ValueError("skinny_strips: wd must be a decode-layout weight (pack_decode_weight)")
+    N, K = wd.shape[0] * 8, wd.shape[1]
+    if not (x2d.dim() == 2 and x2d.shape[1] == K and 1 <= x2d.shape[0] <= STRIPS_MAX_M
+            and x2d.dtype in (torch.float32, torch.float16) and x2d.device == wd.device):
+        raise ValueError(f"skinny_strips: x2d must be [M, {K}] fp32 or fp16 on {wd.device}, 1 <= M <= {STRIPS_MAX_M}")
+    if bias is not None and not (bias.dtype == torch.float32 and bias.numel() == N and bias.device == wd.device):
+        raise ValueError(f"skinny_strips: bias must be fp32 with {N} elements on {wd.device}")
+    x2d = _aligned(x2d)
+    bias = None if bias is None else bias.contiguous()
+    M = x2d.shape[0]
+    out = torch.empty(M, N, device=wd.device, dtype=torch.float32)
+    lib = _clib.load()
+    fn = lib.g16_skinny_strips_f32in if x2d.dtype == torch.float32 else lib.g16_skinny_strips_f16in
+    _clib.check(fn(x2d.data_ptr(), wd.data_ptr(), out.data_ptr(), None if bias is None else bias.data_ptr(),
+                   M, N, K, stream_handle(wd.device.index or 0)), "skinny GEMM (decode layout)")
+    return out
+
+
 # The latest tile-packed rowscale cast per (device index, stream): (weak reference to the tensor the
 # caller named as its source, that tensor's version, (data pointer, M, K, dtype) of the activations
 # cast, owning buffer, packed-cast pointer, row-scales pointer). Consecutive calls that name the same

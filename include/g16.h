@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define G16_ABI_VERSION 15
+#define G16_ABI_VERSION 16
 
 /* Status codes (negative: rejected by the library before any launch). */
 #define G16_OK 0
@@ -243,6 +243,30 @@ int g16_skinny_strip_cols(int M, int N);
 #define G16_NOALLOC_COUNTER_BYTES (64 << 10)
 int g16_skinny_f32in_noalloc(const float* A, const uint16_t* B, float* C, const float* bias, int M,
                              int N, int K, int ksplit, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Skinny GEMM on FastLinear's decode layout (no counterpart kernel in the reference; it serves the
+ * token-by-token branch of FastLinear.forward, src/gtx16_fp16/linear.py:49-64, whose fp16 weight_t
+ * [K,N] is fixed after from_linear, linear.py:30-37). Same semantics as g16_skinny_f32in /
+ * g16_skinny_f16in for 1 <= M <= G16_STRIPS_MAX_M: C[M,N] = A[M,K] @ B16[K,N] + bias in fp32 on
+ * the unquantised activations, fp32 output.
+ * g16_pack_decode_weight writes w_t [K,N] as N/8 strips of 8 columns, each strip all K rows long
+ * and contiguous: wd[(s*K + k)*8 + c] = w_t[k*N + 8*s + c] (K*N fp16 elements, like w_t).
+ * g16_skinny_strips_* run one workgroup of 512 threads per strip over all of K: no split, no
+ * workspace, no counters, C needs no zero-fill, and the result is bitwise reproducible (it differs
+ * from g16_skinny_* in the order of the fp32 additions only). A, wd and C 16-byte aligned;
+ * K and N multiples of 8.
+ */
+#define G16_STRIPS_MAX_M 4
+int g16_pack_decode_weight(const uint16_t* w_t, uint16_t* wd, int K, int N, void* stream);
+int g16_skinny_strips_f32in(const float* A, const uint16_t* wd, float* C, const float* bias, int M,
+                            int N, int K, void* stream);
+int g16_skinny_strips_f16in(const uint16_t* A, const uint16_t* wd, float* C, const float* bias,
+                            int M, int N, int K, void* stream);
+/* 1 where g16_skinny_strips_* is expected to be faster than g16_skinny_* for this product (a
+ * measured rule: M <= 2, or small weights, or fp16 activations at M = 3 and at M = 4 up to
+ * N = 8192); 0 otherwise or for sizes out of range. x_f32: 1 for fp32 activations, 0 for fp16. */
+int g16_skinny_strips_route(int M, int N, int K, int x_f32);
 
 /* ---------------------------------------------------------------------------------------------
  * Clock of the latest GEMM launch (no counterpart in the reference; a measurement aid for the

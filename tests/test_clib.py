@@ -74,6 +74,16 @@ def test_argument_errors_need_no_gpu(lib):
     assert lib.g16_gemm_clock(A + 4, None) == -2
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, 1000.0, None) == -1               # threshold not 2^k
     assert lib.g16_rowscale_f32(A, A, A, 4, 64, -1024.0, None) == -1
+    # the decode layout: M <= 4, K and N multiples of 8, 16-byte alignment, non-NULL operands
+    assert lib.g16_skinny_strips_f32in(A, A, A, None, 5, 64, 64, None) == -1
+    assert lib.g16_skinny_strips_f16in(A, A, A, None, 1, 64, 60, None) == -1
+    assert lib.g16_skinny_strips_f32in(A, A, A + 4, None, 1, 64, 64, None) == -2
+    assert lib.g16_skinny_strips_f32in(None, A, A, None, 1, 64, 64, None) == -3
+    assert lib.g16_skinny_strips_f32in(A, A, A, None, 0, 64, 64, None) == 0
+    assert lib.g16_pack_decode_weight(A, A, 60, 64, None) == -1
+    assert lib.g16_pack_decode_weight(A, A + 8, 64, 64, None) == -2
+    assert lib.g16_pack_decode_weight(A, None, 64, 64, None) == -3
+    assert lib.g16_pack_decode_weight(A, A, 0, 64, None) == 0
 
 
 def test_gemm_size_limits_refused_before_launch(lib):
@@ -183,8 +193,13 @@ def test_fast_extension_matches_the_c_entry_points(lib):
     assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 64, 60, 2048, 256, A, need, None, 0, None, 0, None) == -1
     assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1000.0, 64, 64, 64, 256, None, 0, None, 0, None, 0, None) == -1
     assert fast.mm_t_gemm(A, 1, A, A, 0, None, 1024.0, 0, 64, 2048, 256, A, need, None, 0, None, 0, None) == 0
+    assert fast.skinny_strips_f32in(A, A, A, None, 5, 64, 64, None) == -1
+    assert fast.skinny_strips_f32in(A, A, A + 4, None, 1, 64, 64, None) == -2
+    assert fast.skinny_strips_f32in(A, A, A, None, 0, 64, 64, None) == 0
     with pytest.raises(TypeError):
         fast.skinny_f32in(A, A, A)
+    with pytest.raises(TypeError):
+        fast.skinny_strips_f32in(A, A, A, None, 1, 64, 64)
     with pytest.raises(OverflowError):
         fast.skinny_f32in(A, A, A, None, 1 << 40, 64, 64, 1, None, 0, None, 0, None)
     with pytest.raises(TypeError):
@@ -267,3 +282,15 @@ def test_get_kernel_names_match_reference_kernels():
     assert k.name == "hgemm_f32out" and k.fn is not None and kernels.get_kernel("hgemm_f32out") is k
     with pytest.raises(KeyError):
         kernels.get_kernel("hgemm")
+
+
+def test_decode_layout_route_rule(lib):
+    # g16_skinny_strips_route: the measured rule for FastLinear's decode layout (M <= 2 always; M = 3,
+    # 4 for weights up to 2^22 elements; beyond that only fp16 activations, M = 4 up to N = 8192)
+    r = lib.g16_skinny_strips_route
+    assert r(1, 4096, 4096, 1) == 1 and r(2, 14336, 4096, 1) == 1 and r(1, 8, 8, 0) == 1
+    assert r(3, 2048, 2048, 1) == 1 and r(4, 1024, 3072, 1) == 1
+    assert r(3, 4096, 4096, 1) == 0 and r(4, 4096, 4096, 1) == 0
+    assert r(3, 4096, 4096, 0) == 1 and r(4, 4096, 4096, 0) == 1 and r(3, 14336, 4096, 0) == 1
+    assert r(4, 11008, 4096, 0) == 0 and r(4, 8192, 8192, 0) == 1
+    assert r(5, 64, 64, 0) == 0 and r(0, 64, 64, 1) == 0 and r(1, 0, 64, 1) == 0 and r(1, 64, 0, 1) == 0
