@@ -22,7 +22,9 @@ for M=1 4096x4096 mm_t":
 * ``skinny_m1`` -- the second half of the metric: GB/s of the M=1 K=N=4096 skinny path, kernel
   time from HIP events around a captured HIP graph of launches that rotate over 16 distinct 32 MiB
   weight copies (512 MiB, twice the 256 MB Infinity Cache, so bytes come from HBM), against the
-  8 TB/s HBM peak; plus the per-call mm_t time and its own ``cpu_baseline``.
+  8 TB/s HBM peak; plus the per-call mm_t time and its own ``cpu_baseline``, and the same
+  product on FastLinear's decode layout (``fastlinear_decode_layout``, timed the same way; not the
+  metric, which is mm_t on w_t as given).
 * ``cpu_baseline`` -- the reference's CPU path (torch fp32 matmul, the fallback of ops.py:119)
   on a 4096^3 sample on the host cores of the same run (the skinny half: fp32 addmm at M=1).
 
@@ -258,12 +260,40 @@ def bench_skinny(torch, lib, g, steps: int, warmup: int, dev, copies: int = 16) 
         ms = event_time_ms(graph.replay, reps, torch)
         per_launch.append(ms / copies)
     kern_ms = min(per_launch)
+
+    # FastLinear's decode layout of the same weights (not mm_t's path: mm_t takes w_t as given),
+    # timed the same way
+    wds = []
+    for wi in ws:
+        wd = torch.empty(K * N, dtype=torch.float16, device=dev)
+        _clib_ok(lib.g16_pack_decode_weight(wi.data_ptr(), wd.data_ptr(), K, N, torch.cuda.current_stream(dev).cuda_stream))
+        wds.append(wd)
+    out2 = torch.empty(M, N, dtype=torch.float32, device=dev)
+    graph2 = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        side.wait_stream(torch.cuda.current_stream(dev))
+        for wd in wds:
+            _clib_ok(lib.g16_skinny_strips_f32in(x.data_ptr(), wd.data_ptr(), out2.data_ptr(), b.data_ptr(), M, N, K,
+                                                 side.cuda_stream))
+        side.synchronize()
+        with torch.cuda.graph(graph2, stream=side):
+            cap = torch.cuda.current_stream(dev).cuda_stream
+            for wd in wds:
+                lib.g16_skinny_strips_f32in(x.data_ptr(), wd.data_ptr(), out2.data_ptr(), b.data_ptr(), M, N, K, cap)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph2.replay()
+    torch.cuda.synchronize()
+    strips_ms = min(event_time_ms(graph2.replay, reps, torch) / copies for _ in range(3))
+    del graph2, wds
     return {
         "M": M, "K": K, "N": N,
         "ksplit": ksplit,
         "bytes_per_launch": nbytes,
         "kernel_us": kern_ms * 1e3,
         "kernel_gbs": nbytes / (kern_ms * 1e-3) / 1e9,
+        "fastlinear_decode_layout_kernel_us": strips_ms * 1e3,
+        "fastlinear_decode_layout_kernel_gbs": nbytes / (strips_ms * 1e-3) / 1e9,
         "call_us": call_us,
         "call_gbs": nbytes / (call_us * 1e-6) / 1e9,
         "weight_copies": copies,
@@ -351,6 +381,23 @@ def bench_all(torch, g, steps: int, dev) -> list:
         add(f"C2 skinny {M}x{K}x{N}", M, K, N, 4, 4, True, ms, cpu_fn=lambda: torch.addmm(bias, x, wf),
             extra={"weight_copies": copies, "timing": "per mm_t call"})
         del ws
+        # the same product through FastLinear's token-by-token path (its decode layout where the
+        # library's rule takes it), one layer per weight copy
+        layers = []
+        for _ in range(copies):
+            fl = g.FastLinear(K, N, bias=True, device=dev)
+            with torch.no_grad():
+                fl.weight_t.copy_(w0.to(dev))
+                fl.bias.copy_(bdv)
+            layers.append(fl)
+        lib = _clib_lib()
+        route = "decode layout" if lib.g16_skinny_strips_route(M, N, K, 1) else "split kernel on weight_t"
+        idx = iter(range(1 << 30))
+        with torch.no_grad():
+            ms = _time_call(torch, lambda: layers[next(idx) % copies](xd), max(steps, copies))
+        add(f"C2 FastLinear decode {M}x{K}x{N}", M, K, N, 4, 4, True, ms,
+            extra={"weight_copies": copies, "timing": "per FastLinear call", "route": route})
+        del layers
     # C3: split-K (fp16 A, fp32 out + bias); repeat runs must be bitwise equal
     for (M, K, N) in ((64, 1024, 1024), (64, 4096, 1024)):
         x = randn((M, K), seed=0, dtype=torch.float16)
@@ -635,6 +682,12 @@ def stream_read_rotated(torch, lib, dev, nbytes: int = 32 << 20, copies: int = 1
         del graph
     del bufs
     return {"gbs": best[0], "workgroups_per_cu": best[1], "bytes": nbytes, "copies": copies}
+
+
+def _clib_lib():
+    from gtx16_fp16 import _clib
+
+    return _clib.load()
 
 
 def _clib_ok(status: int) -> None:
@@ -941,6 +994,14 @@ def main(argv=None) -> int:
                 # rotated over 16 buffers and timed like the skinny launches
                 "measured_peak_read_stream_32mib": round(rot["gbs"], 1),
                 "frac_of_measured_peak_32mib": round(sk["kernel_gbs"] / rot["gbs"], 4),
+            },
+            # FastLinear's token-by-token path on its decode layout (same product and bytes; not the
+            # metric, which is mm_t on w_t as given)
+            "fastlinear_decode_layout": {
+                "kernel": "strips_kernel<float,1> (g16_skinny_strips_f32in)",
+                "kernel_us": round(sk["fastlinear_decode_layout_kernel_us"], 3),
+                "GB/s": round(sk["fastlinear_decode_layout_kernel_gbs"], 1),
+                "frac": round(sk["fastlinear_decode_layout_kernel_gbs"] / HBM_PEAK_GBS, 4),
             },
             "bytes_per_launch": sk["bytes_per_launch"],
             "ksplit": sk["ksplit"],

@@ -64,6 +64,7 @@ class FastLinear(nn.Module):
         # decode-layout weight for the token-by-token route and the key of weight_t it was built from
         self._wd: torch.Tensor | None = None
         self._wd_key: tuple | None = None
+        self._wd_ptr = 0
         # prepacked weight for the large-GEMM route and the (pointer, version) of weight_t it was built from
         self._wp: torch.Tensor | None = None
         self._wp_key: tuple | None = None
@@ -123,13 +124,16 @@ class FastLinear(nn.Module):
             self._wp_key = key
         return self._wp
 
-    def _decode_weight(self) -> torch.Tensor:
+    def _decode_weight(self) -> int:
+        # pointer of the decode-layout copy of weight_t, rebuilt when weight_t is another tensor or
+        # was written in place since (its data pointer and version counter)
         w = self.weight_t
-        key = (w.data_ptr(), w._version, w.device)
-        if self._wd is None or self._wd_key != key:
+        key = (w.data_ptr(), w._version)
+        if self._wd_key != key:
             self._wd = pack_decode_weight(w)
             self._wd_key = key
-        return self._wd
+            self._wd_ptr = self._wd.data_ptr()
+        return self._wd_ptr
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         out_dtype = x.dtype if x.dtype in (torch.float32, torch.float16) else torch.float32
@@ -149,7 +153,8 @@ class FastLinear(nn.Module):
                     stream = stream_handle(dev.index or 0)
                     out = torch.empty(*shape[:-1], N, device=dev, dtype=torch.float32)
                     if strips:
-                        pl(x.data_ptr(), self._decode_weight().data_ptr(), out.data_ptr(), bptr, M, N, K, stream)
+                        wd = self._wd_ptr if self._wd_key == (wptr, self.weight_t._version) else self._decode_weight()
+                        pl(x.data_ptr(), wd, out.data_ptr(), bptr, M, N, K, stream)
                     else:
                         bufs = split_buffers(dev, stream, *sizes)
                         pl(x.data_ptr(), wptr, out.data_ptr(), bptr, M, N, K, ksplit, *bufs, stream)
