@@ -10,8 +10,8 @@ import torch.nn.functional as F
 
 from . import _clib
 from .kernels import SKINNY_MAX_M, PreparedCall, split_buffers, stream_handle
-from .ops import (_is_target, _sm_count, is_affected, mm_t, mm_t_prepacked, pack_decode_weight, pack_weight,
-                  prepacked_route, supported)
+from .ops import (STRIPS_MAX_M, _is_target, _sm_count, is_affected, mm_t, mm_t_prepacked, pack_decode_weight,
+                  pack_weight, prepacked_route, skinny_strips, supported)
 
 
 class FastLinear(nn.Module):
@@ -37,7 +37,7 @@ class FastLinear(nn.Module):
     tensor (unmodified, same stream) share its rowscale cast, the last one of which stays cached
     per stream; ``share_cast = False`` turns that off, and ``ops.release_cast_cache()`` frees it.
 
-    Token-by-token calls (fp32 activations, M <= 4 where the library's rule expects a gain) run on a
+    Token-by-token calls (fp32 or fp16 activations, M <= 4 where the library's rule expects a gain) run on a
     second copy of the weight in a strip-major decode layout (8 columns by all of K per strip), built
     on first such call and kept, like the packed copy, outside the state_dict and rebuilt whenever
     ``weight_t`` changes: one workgroup per strip needs no split of K and no exchange of partial sums
@@ -169,10 +169,19 @@ class FastLinear(nn.Module):
         else:
             odt = torch.float32 if out_dtype == torch.float32 else torch.float16
             M = x2.shape[0]
+            b = self.bias
             if self.prepack_weight and M > SKINNY_MAX_M and \
                     prepacked_route(M, self.out_features, self.in_features, x2.device):
-                y = mm_t_prepacked(x2, self.weight_t, self._packed_weight(), self.bias, odt,
+                y = mm_t_prepacked(x2, self.weight_t, self._packed_weight(), b, odt,
                                    _cast_source=x if self.share_cast else None)
+            elif (self.prepack_decode and M <= STRIPS_MAX_M and x2.device == self.weight_t.device
+                  and (b is None or (b.dtype == torch.float32 and b.device == x2.device))
+                  and _clib.load().g16_skinny_strips_route(M, self.out_features, self.in_features,
+                                                           int(x2.dtype == torch.float32))):
+                # token-by-token calls the fast path above does not take (fp16 activations, views):
+                # the decode layout where the library's rule expects a gain
+                self._decode_weight()
+                y = skinny_strips(x2, self._wd, b)
             else:
                 y = mm_t(x2, self.weight_t, self.bias, odt)
         return y.reshape(*shape[:-1], self.out_features).to(out_dtype)

@@ -125,3 +125,32 @@ def test_fast_linear_keeps_the_split_kernel_where_the_rule_says_so(cuda):
     torch.cuda.synchronize()
     assert fl._wd is None and not fl._decode_entry(4, x.device)[5]
     assert oracle.rel_err(_np(y), oracle.skinny(_np(x), _np(fl.weight_t), _np(fl.bias))) <= SKINNY_TOL
+
+
+def test_fast_linear_fp16_activations_take_the_decode_layout(cuda):
+    # fp16 activations skip the fp32 fast path; the general path takes the decode layout for them
+    # too (fp32 product, cast to fp16 at the end like the skinny path's fp16 output)
+    import gtx16_fp16 as g
+
+    torch.manual_seed(1)
+    fl = g.FastLinear.from_linear(nn.Linear(1024, 3072).to(cuda))
+    x = torch.randn(2, 1, 1024, device=cuda).half()
+    with torch.no_grad():
+        y = fl(x)
+    torch.cuda.synchronize()
+    assert fl._wd is not None
+    assert y.dtype == torch.float16 and y.shape == (2, 1, 3072)
+    ref = oracle.skinny(_np(x).reshape(2, 1024), _np(fl.weight_t), _np(fl.bias))
+    assert oracle.rel_err(_np(y.float()).reshape(2, 3072), ref) <= 1e-3
+    fl2 = g.FastLinear.from_linear(nn.Linear(1024, 3072).to(cuda))
+    with torch.no_grad():
+        fl2.weight_t.copy_(fl.weight_t)
+        fl2.bias.copy_(fl.bias)
+        fl2.prepack_decode = False
+        y2 = fl2(x)
+    torch.cuda.synchronize()
+    assert fl2._wd is None
+    # the two routes differ only in the order of the fp32 additions (then one fp16 rounding each):
+    # both within the fp16 output's tolerance of the oracle, and close to each other
+    assert oracle.rel_err(_np(y2.float()).reshape(2, 3072), ref) <= 1e-3
+    assert oracle.rel_err(_np(y.float()), _np(y2.float()).astype(np.float64)) <= 1e-3
