@@ -66,8 +66,10 @@ __global__ __launch_bounds__(kStripThreads) void strips_kernel(const TX* __restr
     for (int j = 0; j < 8; ++j) acc[m][j] = 0.f;
 
   for (int r = k0; r < k1; r += kWave * U) {
-    // Rows at or past k1 re-read the wavefront's last row and contribute nothing: their weights are
-    // replaced by zeros (not multiplied by a zero activation, so inf/NaN weights cannot leak in).
+    // Rows at or past k1 re-read the wavefront's last row (an in-bounds load) and contribute
+    // nothing: both their weights and their activations are replaced by zeros, so the product is
+    // 0 * 0 whatever the row holds (a +-inf or NaN weight or activation of the last row cannot leak
+    // into the columns a second time).
     u32x4 w[U];
     float a[U][MM];
 #pragma unroll
@@ -77,9 +79,10 @@ __global__ __launch_bounds__(kStripThreads) void strips_kernel(const TX* __restr
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const bool live = r + kWave * u + lane < k1;
       const int row = min(r + kWave * u + lane, k1 - 1);
 #pragma unroll
-      for (int m = 0; m < MM; ++m) a[u][m] = act(A, static_cast<long>(m) * K + row);
+      for (int m = 0; m < MM; ++m) a[u][m] = live ? act(A, static_cast<long>(m) * K + row) : 0.f;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {

@@ -292,9 +292,10 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
   // Slices are added in slice order; loads are issued kZBatch slices at a time (for all of the
   // thread's groups) so their latencies overlap. Every slice, this one's included, is read back
   // from the workspace. Sixteen at a time covers the 16 slices of a 4096-row K in one round trip
-  // (graph-timed, 4096^2: M = 4 10.31 -> 10.02 us, M = 8 13.08 -> 12.93 against 8 at a time; a
-  // thread holds at most one group here, so 16 float4 loads in flight fit its registers).
-  constexpr int kZBatch = 16;
+  // (graph-timed, 4096^2: M = 4 10.31 -> 10.02 us, M = 8 13.08 -> 12.93 against 8 at a time). The
+  // batch holds at most 16 loads per thread (64 registers with float4 groups): a thread with two
+  // groups (512-column strips at M = 8) takes 8 slices per round trip.
+  constexpr int kZBatch = kGroupsPerThread > 1 ? (16 / kGroupsPerThread > 0 ? 16 / kGroupsPerThread : 1) : 16;
   V s[kGroupsPerThread];
 #pragma unroll
   for (int i = 0; i < kGroupsPerThread; ++i) s[i] = V{};

@@ -11,7 +11,7 @@ import torch.nn.functional as F
 from . import _clib
 from .kernels import SKINNY_MAX_M, PreparedCall, split_buffers, stream_handle
 from .ops import (STRIPS_MAX_M, _is_target, _sm_count, is_affected, mm_t, mm_t_prepacked, pack_decode_weight,
-                  pack_weight, prepacked_route, skinny_strips, supported)
+                  pack_weight, prepacked_route, skinny_strips, supported, tensor_version)
 
 
 class FastLinear(nn.Module):
@@ -31,41 +31,60 @@ class FastLinear(nn.Module):
 
     On the tile-packed GEMM route (large M) the layer also builds, on first use, a copy of its
     weight in the GEMM's packed layout and keeps it outside the state_dict; it is rebuilt whenever
-    ``weight_t`` is replaced, moved or modified in place. That spends one more fp16 copy of the
-    weight to save the GEMM's transposing LDS reads; ``prepack_weight = False`` (on the class or an
-    instance) turns it off. On the same route, layers called one after another with the same input
-    tensor (unmodified, same stream) share its rowscale cast, the last one of which stays cached
-    per stream; ``share_cast = False`` turns that off, and ``ops.release_cast_cache()`` frees it.
+    ``weight_t`` is replaced, moved or modified in place through torch. That spends one more fp16
+    copy of the weight (the layer then holds as many bytes as the fp32 ``nn.Linear`` it replaced)
+    to save the GEMM's transposing LDS reads; ``prepack_weight = False`` (on the class or an
+    instance) turns it off.
 
-    Token-by-token calls (fp32 or fp16 activations, M <= 4 where the library's rule expects a gain) run on a
-    second copy of the weight in a strip-major decode layout (8 columns by all of K per strip), built
-    on first such call and kept, like the packed copy, outside the state_dict and rebuilt whenever
-    ``weight_t`` changes: one workgroup per strip needs no split of K and no exchange of partial sums
-    between workgroups (4096 x 4096 at M = 1: 8.7 -> 7.3 us; 1024 x 1024: 5.0 -> 3.0 us). Same
-    semantics as the skinny path, with the fp32 additions in another order. ``prepack_decode = False``
-    turns it off.
+    Two more caches are opt-in, because each trades memory or a staleness risk for speed:
+
+    * ``share_cast = True``: large-batch layers called one after another with the same input tensor
+      (a transformer's Q, K and V projections) on one stream reuse the first call's rowscale cast.
+      A cast is reused only while the input is the same live tensor with the same torch version
+      counter; writes that bypass torch's counter (a custom kernel writing through ``data_ptr()``,
+      ``x.data.copy_()``, a serving stack refilling the buffer in place) are not seen and would
+      make the next layer read a stale cast. Inputs created under ``torch.inference_mode()`` carry
+      no version counter and are never shared. ``ops.release_cast_cache()`` frees the cached cast.
+    * ``prepack_decode = True``: token-by-token calls (fp32 or fp16 activations, M <= 4 where the
+      library's rule expects a gain) run on a second copy of the weight in a strip-major decode
+      layout (8 columns by all of K per strip), built on the first such call and rebuilt whenever
+      ``weight_t`` changes: one workgroup per strip needs no split of K and no exchange of partial
+      sums between workgroups (4096 x 4096 at M = 1: 8.7 -> 7.3 us; 1024 x 1024: 5.0 -> 3.0 us).
+      Same semantics as the skinny path, with the fp32 additions in another order. It costs one
+      more fp16 copy of the weight (with the packed copy: three fp16 copies per layer, 1.5x the
+      bytes of the fp32 layer).
+
+    Neither copy is built while the current stream is being captured into a graph (the call takes
+    the route on ``weight_t`` instead); a copy is built eagerly, and the device is synchronised
+    around the build, so the copy is complete before any stream reads it and the one it replaces
+    is no longer read when it is freed. A ``weight_t`` that is an inference tensor (made under
+    ``torch.inference_mode()``) has no version counter: in-place writes to it are not seen (replace
+    the tensor, or call ``release_copies()``).
     """
 
     prepack_weight = True
-    prepack_decode = True
-    # Large-batch calls whose input is the same unmodified tensor as the previous such call on the
-    # stream (a transformer's Q, K and V projections) reuse that call's rowscale cast.
-    share_cast = True
+    # opt-in: a second fp16 copy of the weight in the decode layout (see the class docstring)
+    prepack_decode = False
+    # opt-in: large-batch calls whose input is the same unmodified tensor as the previous such call
+    # on the stream (a transformer's Q, K and V projections) reuse that call's rowscale cast
+    share_cast = False
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True, device=None):
         super().__init__()
         self.in_features, self.out_features = in_features, out_features
-        # (M, device index, prepack_decode) -> (PreparedCall or None, ksplit, (partial, counter) bytes,
-        # weight pointer, bias pointer, decode layout) for the token-by-token fast path; None in the
-        # first field when the weight or bias the pointers name cannot be handed to the kernel (the
-        # call then takes the general path); ksplit 0 and the last field True on the decode-layout
-        # route.
+        # (M, device index, prepack_decode) -> (PreparedCall of the split kernel or None, ksplit,
+        # (partial, counter) bytes, weight pointer, bias pointer, PreparedCall of the decode-layout
+        # kernel or None) for the token-by-token fast path; None in the first field when the weight or
+        # bias the pointers name cannot be handed to the kernel (the call then takes the general
+        # path); the last field is set where the decode layout serves the call.
         self._skinny: dict = {}
-        # decode-layout weight for the token-by-token route and the key of weight_t it was built from
+        # decode-layout weight for the token-by-token route and the (pointer, version, device) of
+        # weight_t it was built from
         self._wd: torch.Tensor | None = None
         self._wd_key: tuple | None = None
         self._wd_ptr = 0
-        # prepacked weight for the large-GEMM route and the (pointer, version) of weight_t it was built from
+        # prepacked weight for the large-GEMM route and the (pointer, version, device) of weight_t it
+        # was built from
         self._wp: torch.Tensor | None = None
         self._wp_key: tuple | None = None
         self.register_buffer("weight_t", torch.empty(in_features, out_features, dtype=torch.float16, device=device))
@@ -101,39 +120,67 @@ class FastLinear(nn.Module):
                   and N % 8 == 0 and w.data_ptr() % 16 == 0 and _is_target(dev.index or 0)
                   and (b is None or (b.dtype == torch.float32 and b.device == dev and b.is_contiguous()
                                      and b.numel() == N)))
-            pl, ksplit, sizes, strips = None, 0, (0, 0), False
+            pl, ksplit, sizes, pls = None, 0, (0, 0), None
             if ok:
                 lib = _clib.load()
-                strips = bool(self.prepack_decode and lib.g16_skinny_strips_route(M, N, K, 1))
-                if strips:
-                    pl = PreparedCall(_clib.fast().skinny_strips_f32in, "skinny GEMM (decode layout)")
-                else:
-                    ksplit = lib.g16_skinny_plan(M, N, K, _sm_count(dev))
-                    pl = PreparedCall(_clib.fast().skinny_f32in, "skinny GEMM")
-                    sizes = (lib.g16_skinny_workspace_bytes(M, N, K, ksplit),
-                             lib.g16_skinny_counter_bytes(M, N, K, ksplit))
-            entry = (pl, ksplit, sizes, w.data_ptr(), bptr, strips)
+                # the split kernel on weight_t always (also the decode layout's stand-in while its copy
+                # cannot be built: under graph capture)
+                ksplit = lib.g16_skinny_plan(M, N, K, _sm_count(dev))
+                pl = PreparedCall(_clib.fast().skinny_f32in, "skinny GEMM")
+                sizes = (lib.g16_skinny_workspace_bytes(M, N, K, ksplit),
+                         lib.g16_skinny_counter_bytes(M, N, K, ksplit))
+                if self.prepack_decode and lib.g16_skinny_strips_route(M, N, K, 1):
+                    pls = PreparedCall(_clib.fast().skinny_strips_f32in, "skinny GEMM (decode layout)")
+            entry = (pl, ksplit, sizes, w.data_ptr(), bptr, pls)
             self._skinny[key] = entry
         return entry
 
-    def _packed_weight(self) -> torch.Tensor:
+    def _weight_key(self) -> tuple:
+        # what a copy of weight_t is valid for: its storage, in-place write counter and device
         w = self.weight_t
-        key = (w.data_ptr(), w._version, w.device)
+        return (w.data_ptr(), tensor_version(w), w.device)
+
+    def _build_copy(self, old: torch.Tensor | None, pack) -> torch.Tensor:
+        # Eager build of a copy of weight_t. Any stream may read a copy, so the device is synchronised
+        # before the old copy is dropped (no kernel still reads it when the allocator reuses it) and
+        # after the new one is written (complete before any stream reads it). Once per weight change.
+        dev = self.weight_t.device
+        if old is not None:
+            torch.cuda.synchronize(old.device)
+        new = pack(self.weight_t)
+        torch.cuda.synchronize(dev)
+        return new
+
+    def _packed_weight(self) -> torch.Tensor | None:
+        # the prepacked copy of weight_t, (re)built when weight_t is another tensor or was written in
+        # place; None when it is not current and the stream is being captured (no build then)
+        key = self._weight_key()
         if self._wp is None or self._wp_key != key:
-            self._wp = pack_weight(w)
+            if torch.cuda.is_current_stream_capturing():
+                return None
+            self._wp = self._build_copy(self._wp, pack_weight)
             self._wp_key = key
         return self._wp
 
     def _decode_weight(self) -> int:
-        # pointer of the decode-layout copy of weight_t, rebuilt when weight_t is another tensor or
-        # was written in place since (its data pointer and version counter)
-        w = self.weight_t
-        key = (w.data_ptr(), w._version)
-        if self._wd_key != key:
-            self._wd = pack_decode_weight(w)
+        # pointer of the decode-layout copy of weight_t, (re)built like the prepacked copy; 0 when it
+        # is not current and the stream is being captured
+        key = self._weight_key()
+        if self._wd is None or self._wd_key != key:
+            if torch.cuda.is_current_stream_capturing():
+                return 0
+            self._wd = self._build_copy(self._wd, pack_decode_weight)
             self._wd_key = key
             self._wd_ptr = self._wd.data_ptr()
         return self._wd_ptr
+
+    def release_copies(self) -> None:
+        """Free the prepacked and decode-layout copies of the weight (rebuilt on demand)."""
+        if self._wp is not None or self._wd is not None:
+            torch.cuda.synchronize(self.weight_t.device)
+        self._wp = self._wd = None
+        self._wp_key = self._wd_key = None
+        self._wd_ptr = 0
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         out_dtype = x.dtype if x.dtype in (torch.float32, torch.float16) else torch.float32
@@ -148,13 +195,16 @@ class FastLinear(nn.Module):
             M = x.numel() // K if shape[-1] == K else -1
             if 0 < M <= SKINNY_MAX_M:
                 dev = x.device
-                pl, ksplit, sizes, wptr, bptr, strips = self._decode_entry(M, dev)
+                pl, ksplit, sizes, wptr, bptr, pls = self._decode_entry(M, dev)
                 if pl is not None:
                     stream = stream_handle(dev.index or 0)
                     out = torch.empty(*shape[:-1], N, device=dev, dtype=torch.float32)
-                    if strips:
-                        wd = self._wd_ptr if self._wd_key == (wptr, self.weight_t._version) else self._decode_weight()
-                        pl(x.data_ptr(), wd, out.data_ptr(), bptr, M, N, K, stream)
+                    wd = 0
+                    if pls is not None:
+                        w = self.weight_t
+                        wd = self._wd_ptr if self._wd_key == (wptr, tensor_version(w), w.device) else self._decode_weight()
+                    if wd:
+                        pls(x.data_ptr(), wd, out.data_ptr(), bptr, M, N, K, stream)
                     else:
                         bufs = split_buffers(dev, stream, *sizes)
                         pl(x.data_ptr(), wptr, out.data_ptr(), bptr, M, N, K, ksplit, *bufs, stream)
@@ -170,17 +220,19 @@ class FastLinear(nn.Module):
             odt = torch.float32 if out_dtype == torch.float32 else torch.float16
             M = x2.shape[0]
             b = self.bias
+            wp = None
             if self.prepack_weight and M > SKINNY_MAX_M and \
                     prepacked_route(M, self.out_features, self.in_features, x2.device):
-                y = mm_t_prepacked(x2, self.weight_t, self._packed_weight(), b, odt,
-                                   _cast_source=x if self.share_cast else None)
+                wp = self._packed_weight()
+            if wp is not None:
+                y = mm_t_prepacked(x2, self.weight_t, wp, b, odt, _cast_source=x if self.share_cast else None)
             elif (self.prepack_decode and M <= STRIPS_MAX_M and x2.device == self.weight_t.device
                   and (b is None or (b.dtype == torch.float32 and b.device == x2.device))
                   and _clib.load().g16_skinny_strips_route(M, self.out_features, self.in_features,
-                                                           int(x2.dtype == torch.float32))):
+                                                           int(x2.dtype == torch.float32))
+                  and self._decode_weight()):
                 # token-by-token calls the fast path above does not take (fp16 activations, views):
                 # the decode layout where the library's rule expects a gain
-                self._decode_weight()
                 y = skinny_strips(x2, self._wd, b)
             else:
                 y = mm_t(x2, self.weight_t, self.bias, odt)

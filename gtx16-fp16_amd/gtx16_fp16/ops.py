@@ -25,6 +25,12 @@ _arch_ok: dict[int, bool] = {}
 _spec_history: set[int] = set()
 
 
+def tensor_version(t: torch.Tensor) -> int | None:
+    """torch's in-place write counter of ``t``; None for an inference tensor (one made under
+    ``torch.inference_mode()``), which has no counter."""
+    return None if t.is_inference() else t._version
+
+
 def _dev_index(device) -> int:
     if device is None:
         return torch.cuda.current_device()
@@ -295,10 +301,13 @@ def release_cast_cache() -> None:
 def _packed_cast(lib, x2d: torch.Tensor, M: int, K: int, dev: torch.device, stream: int, source=None):
     """(owner, packed-cast pointer, row-scales pointer) of x2d's tile-packed rowscale cast, enqueued
     on ``stream``, or the cached one of the previous call on this stream when ``source`` is the same
-    unmodified tensor. Not cached while the stream is being captured into a graph."""
+    unmodified tensor. Not cached while the stream is being captured into a graph, nor for an
+    inference tensor (no version counter to tell whether it was written since)."""
     key = (dev.index or 0, stream)
     meta = (x2d.data_ptr(), M, K, x2d.dtype)
     capturing = torch.cuda.is_current_stream_capturing()
+    if source is not None and source.is_inference():
+        source = None
     if source is not None and not capturing:
         hit = _cast_cache.get(key)
         if hit is not None and hit[0]() is source and hit[1] == source._version and hit[2] == meta:

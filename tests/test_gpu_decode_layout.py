@@ -7,8 +7,12 @@ src/gtx16_fp16/linear.py:49-64, skinny semantics kernels.py:153-219).
   <= 1e-5) for M = 1..4, fp32 and fp16 activations, with and without bias, on shapes with ragged K
   (rows that end inside a wavefront's 64-row group, wavefronts with no rows at all) and N from one
   strip to 11008 columns, and bitwise repeatable.
-* FastLinear takes the route where the library's rule says so, keeps the copy outside its
-  state_dict, and rebuilds it when weight_t is modified in place or replaced.
+* FastLinear (with the opt-in ``prepack_decode``) takes the route where the library's rule says
+  so, keeps the copy outside its state_dict, and rebuilds it when weight_t is modified in place or
+  replaced; it builds no copy under graph capture and works under ``torch.inference_mode()``.
+* Non-finite activations: lanes past the end of a wavefront's rows add nothing, so a +-inf in the
+  last row of a wavefront's range (or at K - 1) gives the oracle's +-inf (or NaN) per column, not a
+  NaN from inf * 0.
 """
 from __future__ import annotations
 
@@ -86,6 +90,8 @@ def test_fast_linear_takes_the_decode_layout_and_rebuilds_it(cuda):
     lib = _clib.load()
     torch.manual_seed(0)
     fl = g.FastLinear.from_linear(nn.Linear(1024, 3072).to(cuda))
+    assert not fl.prepack_decode          # opt-in
+    fl.prepack_decode = True
     assert lib.g16_skinny_strips_route(1, 3072, 1024, 1) == 1
     x = torch.randn(1, 1024, device=cuda)
 
@@ -119,6 +125,7 @@ def test_fast_linear_keeps_the_split_kernel_where_the_rule_says_so(cuda):
     import gtx16_fp16 as g
 
     fl = g.FastLinear.from_linear(nn.Linear(4096, 4096).to(cuda))
+    fl.prepack_decode = True
     x = torch.randn(4, 4096, device=cuda)              # fp32 activations, M = 4, 2^24 weights
     with torch.no_grad():
         y = fl(x)
@@ -134,6 +141,7 @@ def test_fast_linear_fp16_activations_take_the_decode_layout(cuda):
 
     torch.manual_seed(1)
     fl = g.FastLinear.from_linear(nn.Linear(1024, 3072).to(cuda))
+    fl.prepack_decode = True
     x = torch.randn(2, 1, 1024, device=cuda).half()
     with torch.no_grad():
         y = fl(x)
@@ -154,3 +162,109 @@ def test_fast_linear_fp16_activations_take_the_decode_layout(cuda):
     # both within the fp16 output's tolerance of the oracle, and close to each other
     assert oracle.rel_err(_np(y2.float()).reshape(2, 3072), ref) <= 1e-3
     assert oracle.rel_err(_np(y.float()), _np(y2.float()).astype(np.float64)) <= 1e-3
+
+
+def _rows_per_wave(K):
+    # rows per wavefront of the decode kernel: K over its 8 wavefronts in whole 64-row groups
+    return -(-(-(-K // 8)) // 64) * 64
+
+
+def _assert_same_nonfinite(got, want):
+    # same NaN positions, same infinities with the same signs, finite values within the skinny bar
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isposinf(got), np.isposinf(want))
+    assert np.array_equal(np.isneginf(got), np.isneginf(want))
+    fin = np.isfinite(want)
+    if fin.any():
+        assert oracle.rel_err(got[fin], want[fin]) <= SKINNY_TOL
+
+
+@pytest.mark.parametrize("K", [3072, 11008])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_strips_nonfinite_activation_at_a_wavefronts_last_row(ops, cuda, K, M, x_dtype, with_bias):
+    # +inf / -inf at the last row of a wavefront's range (where that wavefront's last batch of row
+    # loads is partial: the lanes past it re-read that row) and at K - 1: every column must be the
+    # oracle's +-inf (NaN only where the weight is 0), not NaN from the dead lanes' inf * 0.
+    N = 1024
+    rpw = _rows_per_wave(K)
+    rows = [min(K, w * rpw + rpw) - 1 for w in range(8) if w * rpw < K] + [K - 1]
+    x = randn((M, K), seed=K + M, dtype=x_dtype)
+    for m in range(M):
+        x[m, rows[(3 * m) % len(rows)]] = float("inf") if m % 2 == 0 else float("-inf")
+    w = randn((K, N), seed=K, scale=0.02, dtype=torch.float16)
+    b = randn((N,), seed=N, scale=0.02) if with_bias else None
+    wd = ops.pack_decode_weight(w.to(cuda))
+    y = ops.skinny_strips(x.to(cuda), wd, None if b is None else b.to(cuda))
+    torch.cuda.synchronize()
+    want = oracle.skinny(_np(x), _np(w), None if b is None else _np(b))
+    assert not np.isfinite(want).any()
+    _assert_same_nonfinite(_np(y).astype(np.float64), want)
+
+
+@pytest.mark.parametrize("K", [3072, 11008])
+@pytest.mark.parametrize("M", [1, 2])
+def test_fast_linear_decode_route_nonfinite_activation(cuda, K, M):
+    # the same through FastLinear's token-by-token fast path on its decode layout
+    import gtx16_fp16 as g
+
+    N = 1024
+    torch.manual_seed(K)
+    fl = g.FastLinear.from_linear(nn.Linear(K, N).to(cuda))
+    fl.prepack_decode = True
+    x = torch.randn(M, K, device=cuda)
+    rpw = _rows_per_wave(K)
+    x[0, rpw - 1] = float("inf")
+    x[M - 1, K - 1] = float("-inf")
+    with torch.no_grad():
+        y = fl(x)
+    torch.cuda.synchronize()
+    assert fl._decode_entry(M, x.device)[5] is not None and fl._wd is not None
+    want = oracle.skinny(_np(x), _np(fl.weight_t), _np(fl.bias))
+    _assert_same_nonfinite(_np(y).astype(np.float64), want)
+
+
+def test_fast_linear_decode_layout_under_inference_mode_and_capture(cuda):
+    # inference_mode: weight_t built there is an inference tensor (no version counter); capture:
+    # no copy is built inside a capture (the split kernel on weight_t serves the call), and the
+    # copy is built on the next eager call. All within the skinny bar of the oracle.
+    import gtx16_fp16 as g
+
+    torch.manual_seed(7)
+    lin = nn.Linear(1024, 1024).to(cuda)
+    x = torch.randn(1, 1024, device=cuda)
+    with torch.inference_mode():
+        fl = g.FastLinear.from_linear(lin)
+        fl.prepack_decode = True
+        y = fl(x)
+        y2 = fl(x.half())
+    torch.cuda.synchronize()
+    assert fl._wd is not None
+    ref = oracle.skinny(_np(x), _np(fl.weight_t), _np(fl.bias))
+    assert oracle.rel_err(_np(y), ref) <= SKINNY_TOL
+    assert oracle.rel_err(_np(y2.float()), oracle.skinny(_np(x.half()), _np(fl.weight_t), _np(fl.bias))) <= 1e-3
+
+    fl2 = g.FastLinear.from_linear(lin)
+    fl2.prepack_decode = True
+    s = torch.cuda.Stream(cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.stream(s):
+        fl2.prepack_decode = False
+        fl2(x)                              # the split kernel's buffers exist on this stream
+        fl2.prepack_decode = True
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            out = fl2(x)
+    torch.cuda.current_stream(cuda).wait_stream(s)
+    assert fl2._wd is None
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert oracle.rel_err(_np(out), ref) <= SKINNY_TOL
+    with torch.no_grad():
+        y3 = fl2(x)
+    torch.cuda.synchronize()
+    assert fl2._wd is not None and oracle.rel_err(_np(y3), ref) <= SKINNY_TOL

@@ -115,8 +115,12 @@ def test_fast_linear_large_batch_uses_prepacked_weight_and_tracks_changes(cuda):
 
 
 def _qkv(cuda, K=768, N=768, seed=0):
+    # three layers with the opt-in shared cast turned on
     torch.manual_seed(seed)
-    return [FastLinearT.from_linear(nn.Linear(K, N).to(cuda)) for _ in range(3)]
+    layers = [FastLinearT.from_linear(nn.Linear(K, N).to(cuda)) for _ in range(3)]
+    for fl in layers:
+        fl.share_cast = True
+    return layers
 
 
 FastLinearT = None
@@ -202,3 +206,69 @@ def test_no_shared_cast_under_graph_capture(ops, cuda):
         torch.cuda.synchronize()
         for a, b in zip(outs, want):
             assert torch.equal(a, b)
+
+
+def test_shared_cast_is_off_by_default(ops, cuda):
+    # share_cast is opt-in: a default layer casts its own input on every call
+    torch.manual_seed(3)
+    layers = [FastLinearT.from_linear(nn.Linear(768, 768).to(cuda)) for _ in range(2)]
+    assert not any(fl.share_cast for fl in layers)
+    x = randn((11264, 768), seed=8).to(cuda)
+    ops.release_cast_cache()
+    with torch.no_grad():
+        got = [fl(x) for fl in layers]
+    assert len(ops._cast_cache) == 0
+    for fl, y in zip(layers, got):
+        assert torch.equal(y, ops.mm_t(x, fl.weight_t, fl.bias))
+
+
+def test_large_batch_under_inference_mode(ops, cuda):
+    # Inference tensors carry no version counter: the prepacked route and the opt-in shared cast
+    # must still run (the cast is then never shared), also for a layer built under inference_mode,
+    # whose weight_t is itself an inference tensor.
+    torch.manual_seed(4)
+    lin = nn.Linear(768, 768).to(cuda)
+    layers = _qkv(cuda, seed=4)
+    x = randn((11264, 768), seed=9).to(cuda)
+    want = _unshared(layers, x)
+    with torch.inference_mode():
+        xi = x.clone()
+        assert xi.is_inference()
+        got = [fl(xi) for fl in layers]
+        built = FastLinearT.from_linear(lin)
+        assert built.weight_t.is_inference()
+        yb = built(xi)
+    torch.cuda.synchronize()
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+    ref = FastLinearT.from_linear(lin)  # the same weights, built outside inference_mode
+    assert torch.equal(yb, ops.mm_t(x, ref.weight_t, ref.bias))
+    assert built._wp is not None
+
+
+def test_no_prepacked_copy_is_built_under_graph_capture(ops, cuda):
+    # The first large-batch call of a layer inside a capture takes mm_t on weight_t (the pack kernel
+    # is not recorded into the graph); replays match eager and the layer builds its copy eagerly later.
+    torch.manual_seed(5)
+    fl = FastLinearT.from_linear(nn.Linear(768, 768).to(cuda))
+    x = randn((11264, 768), seed=10).to(cuda)
+    want = ops.mm_t(x, fl.weight_t, fl.bias)
+    s = torch.cuda.Stream(cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.stream(s):
+        ops.mm_t(x, fl.weight_t, fl.bias)  # the stream's cast scratch exists before capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            out = fl(x)
+    torch.cuda.current_stream(cuda).wait_stream(s)
+    assert fl._wp is None
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+    with torch.no_grad():
+        y = fl(x)
+    torch.cuda.synchronize()
+    assert fl._wp is not None and torch.equal(y, want)
