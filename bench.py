@@ -386,6 +386,7 @@ def bench_all(torch, g, steps: int, dev) -> list:
         layers = []
         for _ in range(copies):
             fl = g.FastLinear(K, N, bias=True, device=dev)
+            fl.prepack_decode = True  # opt-in: the decode-layout copy of the weight
             with torch.no_grad():
                 fl.weight_t.copy_(w0.to(dev))
                 fl.bias.copy_(bdv)
@@ -518,6 +519,7 @@ def bench_overhead(torch, g, dev, n: int = 1000) -> list:
         torch.manual_seed(0)
         lin = nn.Linear(K, N).to(dev)
         fl = g.FastLinear.from_linear(lin)
+        fl.prepack_decode = True  # opt-in: the decode-layout copy of the weight
         x = torch.randn(1, 1, K, device=dev)
         a, b = cost(lambda: lin(x)), cost(lambda: fl(x))
         rows.append({"config": f"decode overhead 1x{K}x{N}", "nn_linear_cpu_us": a[0], "nn_linear_wall_us": a[1],
@@ -541,25 +543,11 @@ def bench_peak(torch, lib, dev) -> list:
     for kind, name, waves_per_simd, iters in (
             (0, "fp32 FMA (VALU)", 8, 20000), (1, "packed fp16 FMA (VALU)", 8, 20000),
             (2, "MFMA f16 32x32x16", 2, 20000), (3, "MFMA f16 16x16x32", 2, 20000),
-            (4, "MFMA f16 32x32x16, random operands", 2, 20000), (5, "MFMA f16 16x16x32, random operands", 2, 20000)):
+            (4, "MFMA f16 32x32x16, random operands", 2, 20000), (5, "MFMA f16 16x16x32, random operands", 2, 20000),
+            (8, "MFMA f16 16x16x32 in the 256x256 tile's order, C4-distributed operands", 2, 10000)):
         blocks = cus * waves_per_simd  # 256-lane workgroups: 4 wavefronts each, one per SIMD
-        out = torch.empty(blocks * 256, device=dev)
-        _clib_ok(lib.g16_peak_run(kind, blocks, 100, out.data_ptr(), stream))
-        torch.cuda.synchronize()
-        best, mhz = float("inf"), 0.0
-        for _ in range(3):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            _clib_ok(lib.g16_peak_run_clocked(kind, blocks, iters, out.data_ptr(), clocks.data_ptr(), stream))
-            e1.record()
-            e1.synchronize()
-            t = e0.elapsed_time(e1) * 1e-3
-            if t < best:
-                cyc, ticks = clocks.tolist()
-                best, mhz = t, (100.0 * cyc / ticks if ticks else 0.0)
-        flop = lib.g16_peak_flops_per_lane_iter(kind) * blocks * 256 * iters
-        rows.append({"peak": name, "TFLOP/s": round(flop / best / 1e12, 1), "ms": round(best * 1e3, 3),
-                     "clock_MHz": round(mhz)})
+        tflops, mhz = time_mfma_probe(torch, lib, dev, kind, blocks, iters)
+        rows.append({"peak": name, "TFLOP/s": round(tflops, 1), "clock_MHz": round(mhz)})
         print(json.dumps(rows[-1]), flush=True)
     for kind, name in ((6, "LDS read, ds_read_b128"), (7, "LDS transposing read, ds_read_b64_tr_b16")):
         for per_cu in (1, 2, 4):  # 32 KB of LDS per workgroup: at most 5 per CU
@@ -609,29 +597,58 @@ def bench_peak(torch, lib, dev) -> list:
     return rows
 
 
-def measured_peaks(torch, lib, dev) -> dict:
-    """The part's own ceilings for the two rooflines, next to the published peaks: the
-    register-only v_mfma_f32_16x16x32_f16 loop on random fp16 operands (bench.py --peak kind 5,
-    the rate a GEMM on real data can reach under the part's power limit, with the clock it held)
-    and the 4 GiB read stream at 16 workgroups per CU. Best of 3 launches after a warm-up each."""
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+def c4_mfma_operands(torch, dev, groups: int, seed: int = 0):
+    """Operands of the GEMM-order MFMA probe (g16_peak_mfma_data) for `groups` workgroups: per
+    lane, two sets of 8 A fragments of fp16(N(0,1)) and 4 B fragments of fp16(N(0, 0.02^2)), the
+    distributions of C4's activations (outlier rows aside) and weights, as int16 bit patterns."""
+    gen = torch.Generator(dev).manual_seed(seed)
+    v = torch.randn(groups, 256, 2, 12, 8, device=dev, generator=gen)
+    v[..., 8:, :] *= 0.02
+    return v.half().view(torch.int16).contiguous()
+
+
+def time_mfma_probe(torch, lib, dev, kind: int, blocks: int, iters: int) -> tuple[float, float]:
+    """(TFLOP/s, MHz) of an MFMA probe (kinds 0-7 through g16_peak_run_clocked; kind 8 is the
+    GEMM-order probe on C4-distributed operands, every workgroup its own): best of 3 launches
+    after a warm-up, with the shader clock workgroup 0's loop held."""
     stream = torch.cuda.current_stream(dev).cuda_stream
     clocks = torch.zeros(2, dtype=torch.int64, device=dev)
-    blocks, iters = cus * 2, 20000
-    out = torch.empty(blocks * 256, device=dev)
-    _clib_ok(lib.g16_peak_run(5, blocks, 100, out.data_ptr(), stream))
+    if kind == 8:
+        ops = c4_mfma_operands(torch, dev, blocks)
+        out = torch.empty(blocks * 256 * 128, device=dev)
+
+        def run(n, clk):
+            return lib.g16_peak_mfma_data(blocks, n, ops.data_ptr(), blocks, out.data_ptr(), clk, stream)
+    else:
+        out = torch.empty(blocks * 256, device=dev)
+
+        def run(n, clk):
+            return lib.g16_peak_run_clocked(kind, blocks, n, out.data_ptr(), clk, stream)
+    _clib_ok(run(100, None))
     best, mhz = float("inf"), 0.0
     for _ in range(3):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        _clib_ok(lib.g16_peak_run_clocked(5, blocks, iters, out.data_ptr(), clocks.data_ptr(), stream))
+        _clib_ok(run(iters, clocks.data_ptr()))
         e1.record()
         e1.synchronize()
         t = e0.elapsed_time(e1) * 1e-3
         if t < best:
             cyc, ticks = clocks.tolist()
             best, mhz = t, (100.0 * cyc / ticks if ticks else 0.0)
-    mfma = lib.g16_peak_flops_per_lane_iter(5) * blocks * 256 * iters / best / 1e12
+    return lib.g16_peak_flops_per_lane_iter(kind) * blocks * 256 * iters / best / 1e12, mhz
+
+
+def measured_peaks(torch, lib, dev) -> dict:
+    """The part's own ceilings for the two rooflines, next to the published peaks: the GEMM's MFMA
+    stream without its memory traffic (g16_peak_mfma_data: the 256x256 tile's per-wavefront MFMA
+    order on C4-distributed operands that change every instruction, two wavefronts per SIMD), with
+    the clock it held; the register-only 16x16x32 loop on fixed uniform random bits (--peak kind 5)
+    beside it; and the 4 GiB read stream at 16 workgroups per CU."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    mfma, mhz = time_mfma_probe(torch, lib, dev, 8, cus * 2, 10000)
+    mfma5, mhz5 = time_mfma_probe(torch, lib, dev, 5, cus * 2, 20000)
     nbytes = 4 << 30
     buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)
     sblocks = cus * 16
@@ -646,7 +663,8 @@ def measured_peaks(torch, lib, dev) -> dict:
         e1.synchronize()
         sbest = min(sbest, e0.elapsed_time(e1) * 1e-3)
     del buf
-    return {"mfma_tflops": mfma, "mfma_clock_mhz": mhz, "stream_gbs": nbytes / sbest / 1e9}
+    return {"mfma_tflops": mfma, "mfma_clock_mhz": mhz, "mfma_uniform_bits_tflops": mfma5,
+            "mfma_uniform_bits_clock_mhz": mhz5, "stream_gbs": nbytes / sbest / 1e9}
 
 
 def stream_read_rotated(torch, lib, dev, nbytes: int = 32 << 20, copies: int = 16) -> dict:
@@ -729,6 +747,15 @@ def bench_bert(torch, g, dev, reps: int = 3, cpu_reps: int = 0) -> dict:
     n = g.patch(model)
     torch.cuda.empty_cache()
     out, t16 = timed()
+    # the same with the opt-in shared activation cast (Q, K and V of a layer share one rowscale cast)
+    fls = [m for m in model.modules() if isinstance(m, g.FastLinear)]
+    for m in fls:
+        m.share_cast = True
+    out_sc, t16_sc = timed()
+    for m in fls:
+        m.share_cast = False
+    same_sc = all(torch.equal(a, b) for a, b in zip(out, out_sc))
+    del out_sc
     # activation ranges the patched linears see (reference bench/diag_ranges.py), on 16 sequences
     from gtx16_fp16.diag import range_hooks, risky
 
@@ -751,6 +778,10 @@ def bench_bert(torch, g, dev, reps: int = 3, cpu_reps: int = 0) -> dict:
             "linears_expected": BERT_LINEARS, "tokens_per_s": round(tokens / t16, 1),
             "fp32_tokens_per_s": round(tokens / t32, 1), "speedup_vs_fp32": round(t32 / t16, 3),
             "ms_per_forward": round(t16 * 1e3, 2), "fp32_ms_per_forward": round(t32 * 1e3, 2),
+            "share_cast": {"tokens_per_s": round(tokens / t16_sc, 1), "ms_per_forward": round(t16_sc * 1e3, 2),
+                           "bitwise_equal_to_default": same_sc,
+                           "what": "FastLinear.share_cast = True (opt-in): consecutive layers on the same input "
+                                   "share its rowscale cast"},
             "linear_TFLOPS_equiv": round(lin_flop / t16 / 1e12, 1),
             "cosine_mean_pooled_min": round(cos[0].min().item(), 8),
             "cosine_cls_min": round(cos[1].min().item(), 8), "activation_ranges": ranges,
@@ -969,6 +1000,10 @@ def main(argv=None) -> int:
             "clock_mhz_back_to_back": round(c4["gemm_b2b_clock_mhz"]),
             "measured_peak_random_operands": round(mp["mfma_tflops"], 1),
             "measured_peak_clock_mhz": round(mp["mfma_clock_mhz"]),
+            "measured_peak_what": "the GEMM tile's MFMA stream (order, operand reuse) on C4-distributed fp16 "
+                                  "operands that change every instruction, registers only (g16_peak_mfma_data)",
+            "measured_peak_uniform_random_bits": round(mp["mfma_uniform_bits_tflops"], 1),
+            "measured_peak_uniform_random_bits_clock_mhz": round(mp["mfma_uniform_bits_clock_mhz"]),
             "frac_of_measured_peak": round(gemm_tflops / mp["mfma_tflops"], 4),
         },
         "rowscale_kernel": {"kernel": "rowscale_kernel<float, packed> (g16_rowscale_pack_f32)", "ms": round(c4["rowscale_kernel_ms"], 5), "GB/s": round(c4["rowscale_kernel_gbs"], 1),

@@ -14,6 +14,14 @@
 //   kind 7: LDS transposing reads, ds_read_b64_tr_b16 (8 bytes per lane), 8 in flight;
 //           kinds 6 and 7 give the LDS read bandwidth a CU sustains for the two fragment reads
 //           the GEMM issues (A fragments are 16-byte reads, B fragments transposing reads);
+//   kind 8 (g16_peak_mfma_data): the 256x256 GEMM tile's own MFMA stream without its memory
+//           traffic. Each wavefront runs the per-step work of one of that tile's wavefronts: 8 A
+//           and 4 B fragments, 32 v_mfma_f32_16x16x32_f16 into 32 accumulators in the tile's
+//           snake order (consecutive MFMAs share one operand, and every MFMA changes the other),
+//           on operand values the caller supplies (the benchmark passes fp16 of N(0,1) for A and
+//           of N(0, 0.02^2) for B, the distributions of its 4096^3 workload), two fragment sets
+//           alternating step by step as the tile's K steps do. Its rate is the ceiling the GEMM's
+//           MFMA stream meets on that data under the part's power limit.
 // and a streaming read of a large buffer (16-byte loads, grid-stride) for HBM bandwidth.
 // Everything stays in registers except the read stream; results are folded into `out` so the
 // compiler cannot drop the work. Workgroup 0's first wavefront can also report the shader clock
@@ -140,6 +148,49 @@ __global__ __launch_bounds__(256) void peak_mfma16(float* out, unsigned long lon
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// Kind 8: per lane, fragment f (0-7: A_f, 8-11: B_(f-8)) of set s is the 8 halves at
+// ops[(((blockIdx.x % ngroups) * 256 + threadIdx.x) * 2 + s) * 12 + f], so with ngroups = the
+// grid every wavefront has operands of its own (the two that share a SIMD included). One iteration
+// is two steps (set 0, set 1)
+// of 32 MFMAs; m = 4 i + jj multiplies A_i by B_j, j = jj on even i and 3 - jj on odd i (the
+// tile's order). All 32 accumulators (4 floats each) are stored: lane t of workgroup b writes
+// out[(b * 256 + t) * 128 + (4 i + j) * 4 + r] = acc[i][j][r], the MFMA's register r of block
+// (i, j): row 4 * (lane / 16) + r, column lane % 16 of the 16 x 16 block.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void peak_mfma_gemm_order(
+    const half8* __restrict__ ops, int ngroups, float* __restrict__ out, unsigned long long* clk, int iters) {
+  const half8* mine = ops + ((blockIdx.x % static_cast<unsigned>(ngroups)) * 256u + threadIdx.x) * 24u;
+  half8 a[2][8], b[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[s][i] = mine[s * 12 + i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[s][j] = mine[s * 12 + 8 + j];
+  }
+  float4v acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+  LoopClock lc;
+  lc.start();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int m = 0; m < 32; ++m) {
+        const int i = m / 4, jj = m % 4, j = (i & 1) ? 3 - jj : jj;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s][i], b[s][j], acc[i][j], 0, 0, 0);
+      }
+  }
+  lc.stop(clk);
+  float4v* o = reinterpret_cast<float4v*>(out + (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) * 128);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[4 * i + j] = acc[i][j];
+}
+
 // LDS read bandwidth: every wavefront reads 8 contiguous pieces of 64 lanes x W bytes (W = 16 for
 // ds_read_b128, 8 for ds_read_b64_tr_b16; contiguous lanes touch distinct banks) from a 32 KB
 // buffer, then waits for them; the reads are inline asm (volatile, with a memory clobber) so the
@@ -220,6 +271,7 @@ extern "C" double g16_peak_flops_per_lane_iter(int kind) {
     case 3: case 5: return 16.0 * 16 * 16 * 32 * 2 / 64;     // 16 MFMA 16x16x32
     case 6: return 8.0 * 16;                         // LDS bytes: 8 ds_read_b128
     case 7: return 8.0 * 8;                          // LDS bytes: 8 ds_read_b64_tr_b16
+    case 8: return 64.0 * 16 * 16 * 32 * 2 / 64;     // two steps of 32 MFMA 16x16x32
     default: return 0.0;
   }
 }
@@ -246,6 +298,17 @@ extern "C" int g16_peak_run_clocked(int kind, int blocks, int iters, float* out,
 
 extern "C" int g16_peak_run(int kind, int blocks, int iters, float* out, void* stream) {
   return g16_peak_run_clocked(kind, blocks, iters, out, nullptr, stream);
+}
+
+extern "C" int g16_peak_mfma_data(int blocks, int iters, const uint16_t* operands, int ngroups, float* out,
+                                  unsigned long long* clocks, void* stream) {
+  // operands: ngroups * 256 * 24 fragments of 8 fp16 values; out: blocks * 256 * 128 floats
+  if (blocks <= 0 || iters < 0 || ngroups <= 0) return G16_E_SHAPE;
+  if (operands == nullptr || out == nullptr) return G16_E_NULL;
+  if (!g16::aligned16(operands) || !g16::aligned16(out)) return G16_E_ALIGN;
+  return g16::launch(g16::peak_mfma_gemm_order, dim3(static_cast<unsigned>(blocks)), dim3(256),
+                     static_cast<hipStream_t>(stream), reinterpret_cast<const g16::half8*>(operands), ngroups, out,
+                     clocks, iters);
 }
 
 extern "C" int g16_stream_read(const void* buf, size_t bytes, int blocks, float* out, void* stream) {

@@ -67,6 +67,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g16_peak_run": (_I, [_I, _I, _I, _P, _P]),
     "g16_peak_run_clocked": (_I, [_I, _I, _I, _P, _P, _P]),
     "g16_stream_read": (_I, [_P, _SZ, _I, _P, _P]),
+    "g16_peak_mfma_data": (_I, [_I, _I, _P, _I, _P, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -294,11 +294,21 @@ int g16_gemm_clock(unsigned long long* dst, void* stream);
  * shader clock cycles and into clocks[1] the 100 MHz reference ticks of workgroup 0's loop.
  * g16_stream_read reads `bytes` (a multiple of 16, 16-byte aligned buffer) once with 16-byte
  * loads from `blocks` workgroups of 256 lanes; `out` holds blocks * 256 floats.
+ * g16_peak_mfma_data (kind 8 of g16_peak_flops_per_lane_iter) runs the 256x256 GEMM tile's per-
+ * wavefront MFMA stream (8 A x 4 B fragments, 32 v_mfma_f32_16x16x32_f16 per step in the tile's
+ * snake order, two fragment sets alternating per step) on caller-supplied operands, `iters`
+ * iterations of two steps, from `blocks` workgroups of 256 lanes. `operands` (16-byte aligned)
+ * holds ngroups * 256 * 24 fragments of 8 fp16 values: fragment f (0-7 A, 8-11 B) of set s for
+ * lane t of workgroup b is operands[(((b % ngroups) * 256 + t) * 2 + s) * 12 + f]. `out`
+ * (16-byte aligned) receives blocks * 256 * 128 floats: lane t of workgroup b stores accumulator
+ * (i, j) register r at out[(b * 256 + t) * 128 + (4 i + j) * 4 + r]. `clocks` as above.
  */
 double g16_peak_flops_per_lane_iter(int kind);
 int g16_peak_run(int kind, int blocks, int iters, float* out, void* stream);
 int g16_peak_run_clocked(int kind, int blocks, int iters, float* out, unsigned long long* clocks, void* stream);
 int g16_stream_read(const void* buf, size_t bytes, int blocks, float* out, void* stream);
+int g16_peak_mfma_data(int blocks, int iters, const uint16_t* operands, int ngroups, float* out,
+                       unsigned long long* clocks, void* stream);
 
 #ifdef __cplusplus
 }
