@@ -127,3 +127,34 @@ def test_skinny_config_covers_k():
         nstrips = (N + cols - 1) // cols
         assert gy == gz == 1 and gx % nstrips == 0
         assert (gx // nstrips) * rows >= K > (gx // nstrips - 1) * rows
+
+
+def test_fast_linear_caches_are_opt_in_and_cpu_layers_build_none():
+    # The decode-layout copy and the shared activation cast are off unless a caller turns them on;
+    # a layer on the CPU (torch fallback) never builds a weight copy, whatever the flags.
+    assert g.FastLinear.prepack_decode is False and g.FastLinear.share_cast is False
+    assert g.FastLinear.prepack_weight is True
+    fl = g.FastLinear.from_linear(nn.Linear(64, 48))
+    fl.prepack_decode = fl.share_cast = True
+    with torch.no_grad():
+        fl(torch.randn(1, 64))
+        fl(torch.randn(300, 64))
+    assert fl._wp is None and fl._wd is None
+    fl.release_copies()  # nothing to free: no synchronisation needed, no error on a CPU layer
+    assert fl._wp is None and fl._wd is None
+
+
+def test_tensor_version_of_inference_tensors():
+    # inference tensors carry no version counter: the caches key them as None instead of raising
+    t = torch.zeros(4)
+    v0 = ops.tensor_version(t)
+    t.add_(1)
+    assert ops.tensor_version(t) == v0 + 1
+    with torch.inference_mode():
+        ti = torch.zeros(4)
+        assert ti.is_inference() and ops.tensor_version(ti) is None
+        with torch.no_grad():
+            fl = g.FastLinear.from_linear(nn.Linear(16, 8))
+        assert fl.weight_t.is_inference()
+        y = fl(torch.randn(2, 16))  # CPU fallback under inference_mode
+    assert y.shape == (2, 8)
