@@ -574,3 +574,36 @@ def test_mm_t_one_call_equals_separate_launches(lib, g, cuda, M, K, N, in_dtype,
     bits = torch.int32 if out_dtype == torch.float32 else torch.int16
     assert torch.isfinite(y).all()
     assert torch.equal(y.view(bits), ref.view(bits))
+
+
+def _same_nonfinite_pattern(got, want):
+    # NaN positions, infinity positions and signs equal; finite entries within the skinny bar
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isposinf(got), np.isposinf(want))
+    assert np.array_equal(np.isneginf(got), np.isneginf(want))
+    fin = np.isfinite(want)
+    if fin.any():
+        assert oracle.rel_err(got[fin], want[fin]) <= SKINNY_TOL
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("K,N", [(3072, 1024), (11008, 1024), (1024, 8704)])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.float16])
+def test_skinny_nonfinite_activations_at_slice_edges(g, lib, cuda, M, K, N, x_dtype):
+    # mm_t's skinny path (M <= 8) on the split kernel: +-inf activations at the first and last row of
+    # the planned K slices and at K - 1 reach the output as the oracle's +-inf (NaN only where the
+    # weight is zero or both signs meet), not as a NaN from rows a lane re-reads and skips
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    ks = lib.g16_skinny_plan(M, N, K, cus)
+    slice_rows = -(-K // ks)
+    x = randn((M, K), seed=K + M, dtype=x_dtype)
+    edges = sorted({0, slice_rows - 1, slice_rows, min(K - 1, 2 * slice_rows - 1), K - 1})
+    for m in range(M):
+        x[m, edges[m % len(edges)]] = float("inf") if m % 2 == 0 else float("-inf")
+    w = randn((K, N), seed=K, scale=0.02, dtype=torch.float16)
+    b = randn((N,), seed=N, scale=0.02)
+    y = g.mm_t(x.to(cuda), w.to(cuda), b.to(cuda), torch.float32)
+    torch.cuda.synchronize()
+    want = oracle.skinny(_np(x), _np(w), _np(b))
+    assert not np.isfinite(want).any()
+    _same_nonfinite_pattern(_np(y).astype(np.float64), want)
