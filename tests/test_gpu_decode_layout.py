@@ -221,7 +221,8 @@ def test_fast_linear_decode_route_nonfinite_activation(cuda, K, M):
         y = fl(x)
     torch.cuda.synchronize()
     assert fl._decode_entry(M, x.device)[5] is not None and fl._wd is not None
-    want = oracle.skinny(_np(x), _np(fl.weight_t), _np(fl.bias))
+    with np.errstate(invalid="ignore"):  # at M = 1 the row holds both infinities: NaN columns expected
+        want = oracle.skinny(_np(x), _np(fl.weight_t), _np(fl.bias))
     _assert_same_nonfinite(_np(y).astype(np.float64), want)
 
 
