@@ -44,6 +44,8 @@ namespace {
 constexpr int kWaves = 8;        // wavefronts per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMinRows = 8;      // the plan gives every wavefront at least this many rows
+constexpr int kMfBatch = 32;     // K rows per batch of the matrix-core form
+constexpr int kMfMaxBatches = 4; // ... its activations held in registers: up to 128 rows per wavefront
 
 // Launch schedule of the kernel:
 //   cols   -- columns of the strip a workgroup owns: 512 (one 1 KB row per load instruction) or
@@ -92,7 +94,27 @@ __device__ inline void fma_row(float (&acc)[MM][8], const float (&a)[MM], u32x4 
     for (int j = 0; j < 8; ++j) acc[m][j] = fmaf(a[m], wf[j], acc[m][j]);
 }
 
-template <typename TX, int MM, class S>
+// Two fp16 parts of a finite x (|x| < 2^15 after the row scaling): hi is x rounded toward zero to
+// fp16, lo the rest rounded to nearest, so |x - hi - lo| <= 2^-21 |x| (<= 2^-25 where lo is
+// subnormal), and an fp16 x gives hi = x. Both parts carry x's sign: a part that would be zero for
+// a nonzero x is the smallest subnormal (2^-24) with x's sign instead (an error of <= 2^-23,
+// negligible next to a row whose largest |x| is >= 2^14). An infinite weight times (hi, lo)
+// therefore gives the infinity the fp32 product gives, never inf - inf; x = +-0 gives (+-0, 0), and
+// 0 * inf is NaN either way.
+__device__ inline void split_hi_lo(float x, _Float16& hi, _Float16& lo) {
+  const uint16_t tiny = static_cast<uint16_t>(((__float_as_uint(x) >> 16) & 0x8000u) | 1u);
+  uint16_t hb = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  hb -= fabsf(static_cast<float>(__builtin_bit_cast(_Float16, hb))) > fabsf(x) ? 1 : 0;  // toward zero
+  const uint16_t lb = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x - static_cast<float>(__builtin_bit_cast(_Float16, hb))));
+  const bool hz = (hb & 0x7fffu) == 0, xz = x == 0.f;
+  hi = __builtin_bit_cast(_Float16, hz ? (xz ? hb : tiny) : hb);
+  lo = __builtin_bit_cast(_Float16, hz ? (xz ? static_cast<uint16_t>(0u) : tiny) : ((lb & 0x7fffu) == 0 ? tiny : lb));
+}
+
+// MF (launched by use_mf: M = 8, 256-column strips, 32..128 K rows per wavefront): a wavefront
+// whose activations are all finite multiplies on the matrix cores (below); one with an inf or NaN
+// among them takes the fp32 FMA loop.
+template <typename TX, int MM, class S, bool MF = false>
 __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__ A, const _Float16* __restrict__ B,
                                                           float* __restrict__ C, const float* __restrict__ bias,
                                                           float* __restrict__ part, uint32_t* __restrict__ counters,
@@ -133,7 +155,134 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
     }
   };
 
-  if (col < N) {
+  // Matrix-core form (MF): one v_mfma_f32_16x16x32_f16 computes 16 A rows x 16 columns x 32 K
+  // rows. Its A rows 0-7 are the fp16 hi parts of the (row-scaled) activations, rows 8-15 their lo
+  // parts (split_hi_lo), so C[m] + C[m + 8] is the fp32-accurate product for m < 8: the products
+  // of fp16 parts are exact, and the fp32 FMAs per weight and row become ~100 VALU instructions per
+  // 32 rows. Each row m is scaled by 2^-e_m (exact) so its largest |x| over the wavefront's rows
+  // lies in [2^14, 2^15), and the partial sum is scaled back by 2^e_m.
+  //   A batch is 32 K rows (16 loads: lanes 0-31 row r + 2u, lanes 32-63 row r + 2u + 1, 8 columns
+  // each, as in the FMA loop). v_permlane16_swap on loads 2p and 2p + 1 leaves in load 2p + s,
+  // lane l: columns 8 (16 s + l % 16) .. +7 of row r + 4p + sigma(l / 16), sigma = (0, 2, 1, 3).
+  // So lane l's B fragment for column 8 (16 s + l % 16) + j is half j of loads s, 2 + s, .., 14 + s,
+  // K rows r + 4t + sigma(l / 16) for t = 0..7, and its A fragment holds the activations of those
+  // rows; the 16 MFMAs (s, j) of a batch share the A fragment. Rows past the wavefront's range
+  // have zero weights (their loads re-read its last row and are replaced by zeros) and zero
+  // activations.
+  bool fma_loop = true;
+  if constexpr (MF) {
+    static_assert(kRowsPerLoad == 2 && MM >= 2 && MM <= 8, "matrix-core form: 256-column strips, 2 <= M <= 8");
+    const int g = lane >> 4, n16 = lane & 15;
+    const int sig = g == 1 ? 2 : (g == 2 ? 1 : g);
+    const int am = n16 & 7;       // the activation row of this lane's A fragment
+    const bool alo = n16 >= 8;    // ... its lo parts (A rows 8-15)
+    const int nb = (k1 - k0 + kMfBatch - 1) / kMfBatch;
+    const bool col_ok = col < N;
+    const _Float16* bp = B + min(col, N - 8);
+    // 16 weight loads of the batch at row r: rows past the wavefront's range re-read its last row
+    // (their values are replaced by zeros once they have landed)
+    u32x4 w[16];
+    auto load_batch = [&](int r) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int row = r + 2 * u + sub;
+        w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp + static_cast<size_t>(min(row, k1 - 1)) * N));
+      }
+    };
+    float xr[kMfMaxBatches][8];
+    float amax = 0.f;
+    if (nb <= kMfMaxBatches && rows_per_wave >= kMfBatch) {
+      // The first batch's weights stream while the activations come in (a wavefront that falls
+      // back to the FMA loop drops them). Every activation this lane's A fragments need is then
+      // loaded: rows past the wavefront's range (and rows am >= M) are 0.
+      load_batch(k0);
+#pragma unroll
+      for (int bt = 0; bt < kMfMaxBatches; ++bt)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int row = k0 + kMfBatch * bt + 4 * t + sig;
+          xr[bt][t] = (bt < nb && am < MM && row < k1) ? x_at(A, static_cast<size_t>(am) * K + row) : 0.f;
+        }
+      // |x| of row am over the wavefront's rows (the 4 lanes of each row combined); an inf or NaN
+      // sends the wavefront to the FMA loop
+      bool bad = false;
+#pragma unroll
+      for (int bt = 0; bt < kMfMaxBatches; ++bt)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const float v = fabsf(xr[bt][t]);
+          bad = bad || !(v <= 3.402823466e38f);
+          amax = fmaxf(amax, v);
+        }
+      amax = fmaxf(amax, __shfl_xor(amax, 16));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      fma_loop = __any(bad);
+    }
+    if (!fma_loop) {
+      const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) - 15 : 0;  // amax * 2^-e in [2^14, 2^15)
+      float4v acc2[2][8];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc2[s][j] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int bt = 0; bt < kMfMaxBatches; ++bt) {
+        if (bt >= nb) break;
+        const int r = k0 + kMfBatch * bt;
+        if (bt > 0) load_batch(r);
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (!col_ok || r + 2 * u + sub >= k1) w[u] = u32x4{0u, 0u, 0u, 0u};
+        half8 af;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          _Float16 hi, lo;
+          split_hi_lo(__builtin_ldexpf(xr[bt][t], -e), hi, lo);
+          af[t] = alo ? lo : hi;
+        }
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(w[2 * p][d], w[2 * p + 1][d], false, false);
+            w[2 * p][d] = sw[0];
+            w[2 * p + 1][d] = sw[1];
+          }
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            half8 bf;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) bf[t] = __builtin_bit_cast(half8, w[2 * t + s])[j];
+            acc2[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc2[s][j], 0, 0, 0);
+          }
+      }
+      // Lane l, register i of acc2[s][j]: A row 4 (l / 16) + i, column 8 (16 s + l % 16) + j, i.e. the
+      // hi part of activation row m = 4 (l / 16 % 2) + i in lanes 0-31 and its lo part in lanes
+      // 32-63. Each lane writes its 8 consecutive columns as two 16-byte writes, scaled back by
+      // 2^e_m (lane m holds e_m): the hi parts into this wavefront's first partial row of the LDS
+      // reduction, the lo parts into its second, which the reduction adds. (One 4-byte write per
+      // value made 8-way bank conflicts: 9 us of a 26 us M = 8 launch.)
+      const int mrow = 4 * (g & 1);
+      int er[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) er[i] = __shfl(e, mrow + i);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (mrow + i >= MM) continue;
+          float* dst = &red[kRowsPerLoad * wave + (g >> 1)][mrow + i][(16 * s + n16) * 8];
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            *reinterpret_cast<float4v*>(dst + 4 * h) =
+                float4v{__builtin_ldexpf(acc2[s][4 * h][i], er[i]), __builtin_ldexpf(acc2[s][4 * h + 1][i], er[i]),
+                        __builtin_ldexpf(acc2[s][4 * h + 2][i], er[i]), __builtin_ldexpf(acc2[s][4 * h + 3][i], er[i])};
+        }
+    }
+  }
+  if (fma_loop && col < N) {
     constexpr int U = S::loads;
     constexpr int RB = U * kRowsPerLoad;  // rows of a batch
     const _Float16* bp = B + col + static_cast<size_t>(sub) * N;
@@ -219,10 +368,12 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const TX* __restrict__
   // 16-byte coherent accesses; single columns below that): group g is row g / (kStripCols / kGW),
   // columns strip*kStripCols + kGW*(g % (kStripCols / kGW)) .., summed over the partial rows in
   // order. Every row of A goes through LDS in the same round, so one barrier serves all of them.
+  if (fma_loop) {
 #pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    *reinterpret_cast<float4v*>(&red[part_row][m][lcol]) = float4v{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
-    *reinterpret_cast<float4v*>(&red[part_row][m][lcol + 4]) = float4v{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
+    for (int m = 0; m < MM; ++m) {
+      *reinterpret_cast<float4v*>(&red[part_row][m][lcol]) = float4v{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+      *reinterpret_cast<float4v*>(&red[part_row][m][lcol + 4]) = float4v{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
+    }
   }
   __syncthreads();
   constexpr int kGW = MM >= 4 ? 4 : 1;
@@ -374,8 +525,18 @@ SkinnyFn<TX> skinny_fn_w(int M) {
     default: return skinny_kernel<TX, 8, typename SchedFor<8, COLS>::type>;
   }
 }
+// The matrix-core form (skinny_kernel's MF) runs where it pays: M = 8 on 256-column strips with
+// 32..128 K rows per wavefront. Graph-timed against the FMA loop, weights rotated past the
+// Infinity Cache, us (K x N): 4096 x 4096 12.69 vs 12.95, 11008 x 4096 20.50 vs 25.52, 14336 x 4096
+// 24.80 vs 29.29, 4096 x 8192 16.52 vs 19.18. Smaller M lose: one batch per wavefront leaves the
+// matrix-core work and the hi/lo split exposed next to the FMAs they replace (M = 7, 4096^2:
+// 12.62 vs 11.24; M = 2..6: 1.5-3 us slower); so do wavefronts with fewer rows than a batch.
+bool use_mf(int M, int cols, int rows_per_wave) {
+  return M == 8 && cols == 256 && rows_per_wave >= kMfBatch && rows_per_wave <= kMfBatch * kMfMaxBatches;
+}
 template <typename TX>
-SkinnyFn<TX> skinny_fn(int M, int cols) {
+SkinnyFn<TX> skinny_fn(int M, int cols, bool mf) {
+  if (mf) return skinny_kernel<TX, 8, typename SchedFor<8, 256>::type, true>;
   return cols == 256 ? skinny_fn_w<TX, 256>(M) : skinny_fn_w<TX, 512>(M);
 }
 
@@ -436,7 +597,7 @@ int skinny_launch(const TX* A, const uint16_t* B, float* C, const float* bias, i
     part = static_cast<float*>(ws);
   }
   const dim3 grid(static_cast<unsigned>(nstrips) * static_cast<unsigned>(sp.ksplit)), block(kThreads);
-  return launch(skinny_fn<TX>(M, cols), grid, block, static_cast<hipStream_t>(stream), A,
+  return launch(skinny_fn<TX>(M, cols, use_mf(M, cols, sp.rows_per_wave)), grid, block, static_cast<hipStream_t>(stream), A,
                 reinterpret_cast<const _Float16*>(B), C, bias, part, counters, N, K, sp.rows_per_wave, sp.ksplit,
                 nstrips);
 }
