@@ -134,6 +134,31 @@ def test_persistent_grid_at_bert_shapes(g, cuda, M, K, N):
     assert oracle.rel_err(_np(y)[rows], ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("M,K,N", [(65636, 768, 776), (40000, 1032, 1288)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_persistent_grid_partial_tiles(g, lib, cuda, M, K, N, out_dtype):
+    # A persistent grid (more 256x256 tiles than CUs) whose last tile row and column are partial and
+    # whose last K step is partial (K = 1032): its C stores are the non-temporal buffer stores (16
+    # bytes for fp32 out, 8 for fp16), bounds-guarded per row and 4-column chunk like the plain ones.
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    assert lib.g16_hgemm_use_packed(M, N, K, cus) == 1
+    tiles = -(-M // 256) * -(-N // 256)
+    assert tiles > cus
+    x = randn((M, K), seed=11).to(cuda)
+    x[M - 1] *= 4000.0  # a rescaled row in the partial tile row
+    w = randn((K, N), seed=12, scale=0.02, dtype=torch.float16).to(cuda)
+    b = randn((N,), seed=13, scale=0.02).to(cuda)
+    y = g.mm_t(x, w, b, out_dtype)
+    y2 = g.mm_t(x, w, b, out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    rows = np.sort(np.random.default_rng(M + K).choice(M, 256, replace=False))
+    rows = np.unique(np.concatenate([rows, [0, 255, 256, M - 257, M - 256, M - 2, M - 1]]))
+    want = oracle.mm_t(_np(x)[rows], _np(w), _np(b), "float16" if out_dtype == torch.float16 else "float32")
+    assert np.isfinite(_np(y)[rows]).all()
+    assert oracle.rel_err(_np(y)[rows], want) <= GEMM_TOL
+
+
 CASES16 = ("skinny_m3", "skinny_m8", "gemm_m12", "gemm_m9", "skinny_tie16", "gemm_tie16")
 
 
