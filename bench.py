@@ -399,6 +399,28 @@ def bench_all(torch, g, steps: int, dev) -> list:
         add(f"C2 FastLinear decode {M}x{K}x{N}", M, K, N, 4, 4, True, ms,
             extra={"weight_copies": copies, "timing": "per FastLinear call", "route": route})
         del layers
+    # M = 8 through mm_t, where the skinny kernel multiplies on the matrix cores (32..128 K rows per
+    # wavefront on 256-column strips; an fp16 hi/lo split of the activations)
+    lib = _clib_lib()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    for (M, K, N) in ((8, 4096, 4096), (8, 11008, 4096)):
+        x = randn((M, K), seed=0)
+        w0 = randn((K, N), seed=1, scale=0.02, dtype=torch.float16)
+        bias = randn((N,), seed=2, scale=0.02)
+        wf = w0.float()
+        xd, bdv = x.to(dev), bias.to(dev)
+        copies = max(16, (512 << 20) // (K * N * 2))
+        ws = [w0.to(dev) for _ in range(copies)]
+        ks = lib.g16_skinny_plan(M, N, K, cus)
+        rpw = -(-(-(-K // ks)) // 8)
+        form = ("matrix cores" if lib.g16_skinny_strip_cols(M, N) == 256 and 32 <= rpw <= 128
+                else "fp32 FMA loop")
+        idx = iter(range(1 << 30))
+        ms = _time_call(torch, lambda: g.mm_t(xd, ws[next(idx) % copies], bdv, torch.float32), max(steps, copies))
+        add(f"skinny {M}x{K}x{N}", M, K, N, 4, 4, True, ms, cpu_fn=lambda: torch.addmm(bias, x, wf),
+            extra={"weight_copies": copies, "timing": "per mm_t call", "form": form, "ksplit": ks,
+                   "rows_per_wavefront": rpw})
+        del ws
     # C3: split-K (fp16 A, fp32 out + bias); repeat runs must be bitwise equal
     for (M, K, N) in ((64, 1024, 1024), (64, 4096, 1024)):
         x = randn((M, K), seed=0, dtype=torch.float16)
