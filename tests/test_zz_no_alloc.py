@@ -1,8 +1,10 @@
 """GPU test of g16_skinny_f32in_noalloc, the allocation-free variant of g16_skinny_f32in: through the
 C ABI, its output is bitwise equal to the buffered entry point's on the same plan (same kernels,
 same summation order), on consecutive calls whose second input is smaller than the first (the
-static scratch keeps the first call's contents), and within 1e-5 of the fp64 oracle. Splits that do
-not fit the static scratch are refused before any launch."""
+static scratch keeps the first call's contents), and within 1e-5 of the fp64 oracle. The first call
+is M = 8 at 4096^2, which runs the matrix-core form of the skinny kernel (16 K slices on 256-column
+strips); the FMA-loop form follows at M = 4 and M = 1. Splits that do not fit the static scratch are
+refused before any launch."""
 from __future__ import annotations
 
 import numpy as np
@@ -36,9 +38,9 @@ def _buffered(lib, x, w, b, ks, st):
 def test_noalloc_matches_the_buffered_entry_point(lib, cuda):
     cus = torch.cuda.get_device_properties(cuda).multi_processor_count
     st = torch.cuda.current_stream(cuda).cuda_stream
-    # larger call first, then a smaller one: M, K and N all shrink, so stale partials and a
+    # larger call first, then smaller ones: M, K and N all shrink, so stale partials and a
     # different strip count would show if the scratch were not handled per call
-    for seed, (M, K, N) in enumerate(((4, 4096, 4096), (1, 1024, 3072), (4, 4096, 4096))):
+    for seed, (M, K, N) in enumerate(((8, 4096, 4096), (4, 4096, 4096), (1, 1024, 3072), (4, 4096, 4096))):
         x = randn((M, K), seed=10 + seed).to(cuda)
         w = randn((K, N), seed=20 + seed, scale=0.02, dtype=torch.float16).to(cuda)
         b = randn((N,), seed=30 + seed, scale=0.02).to(cuda)
