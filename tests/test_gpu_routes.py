@@ -14,6 +14,9 @@ exactly as configured.
   at the BERT-base linear shapes (sampled rows). The tile
   each case runs on is the library's own report (g16_hgemm_tile), so a plan change that moves a
   case to another tile fails here instead of silently dropping that tile from the tests.
+* Rows holding +-inf or NaN (at tile-row edges and at K - 1), an all-zero row and rescaled rows
+  through the tile-packed route (both 256-row tiles, one round and persistent; fp32 and fp16 x and
+  out): exactly the oracle's non-finite pattern, every other row within the GEMM bar.
 * The fp16-output golden fixtures (exact rational results, tests/golden/make_golden.py).
 
 Every result is checked against the fp64 oracle: relative Frobenius error <= 1e-3 on the GEMM
@@ -157,6 +160,45 @@ def test_persistent_grid_partial_tiles(g, lib, cuda, M, K, N, out_dtype):
     want = oracle.mm_t(_np(x)[rows], _np(w), _np(b), "float16" if out_dtype == torch.float16 else "float32")
     assert np.isfinite(_np(y)[rows]).all()
     assert oracle.rel_err(_np(y)[rows], want) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("M,K,N,tile", [(2600, 2056, 2824, (256, 256)), (4096, 1032, 4104, (256, 256)),
+                                        (2048, 2056, 3080, (256, 128))])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.float16])
+def test_packed_route_nonfinite_zero_and_rescaled_rows(g, lib, cus, cuda, M, K, N, tile, x_dtype):
+    # The tile-packed route (rowscale_pack cast, then the 256-row GEMM; past one round a persistent
+    # grid) with rows holding +inf, -inf or NaN, at tile-row edges and at K - 1, next to an all-zero
+    # row and rescaled rows. An infinite row's scale is +inf and its cast 0 * inf = NaN, so its
+    # output row is NaN; a NaN row's |max| ignores the NaN and its output row is NaN too. The
+    # non-finite pattern must be the oracle's exactly, and no other row may be touched by it.
+    if cus != 256:
+        pytest.skip(f"the route table is for 256 CUs (this device has {cus})")
+    assert lib.g16_hgemm_use_packed(M, N, K, cus) == 1
+    assert planned_tile(lib, M, N, K, cus) == tile
+    x = randn((M, K), seed=31)
+    special = {5: ("inf", 7), 255: ("nan", 100), 256: ("inf", K - 1), 300: ("nan", 0), 301: ("-inf", K - 1),
+               M - 1: ("-inf", K // 2)}
+    for r, (v, k) in special.items():
+        x[r, k] = float(v)
+    x[777 % M] = 0.0           # an all-zero row
+    x[1000 % M, 3] = 3.0e4     # rescaled rows (exponent 5), fp16-representable
+    x[257, K - 1] = -2.5e4
+    x = x.to(x_dtype)
+    w = randn((K, N), seed=32, scale=0.02, dtype=torch.float16)
+    b = randn((N,), seed=33, scale=0.02)
+    for out_dtype, name in ((torch.float32, "float32"), (torch.float16, "float16")):
+        y = g.mm_t(x.to(cuda), w.to(cuda), b.to(cuda), out_dtype)
+        torch.cuda.synchronize()
+        rows = np.sort(np.random.default_rng(M + N).choice(M, 192, replace=False))
+        rows = np.unique(np.concatenate([rows, list(special), [777 % M, 1000 % M, 257, 0, 254, 302, M - 2]]))
+        got = _np(y)[rows].astype(np.float64)
+        want = oracle.mm_t(_np(x)[rows], _np(w), _np(b), name).astype(np.float64)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(np.isposinf(got), np.isposinf(want))
+        assert np.array_equal(np.isneginf(got), np.isneginf(want))
+        bad = np.isin(rows, list(special))
+        assert np.isnan(want[bad]).all() and np.isfinite(want[~bad]).all()
+        assert oracle.rel_err(got[~bad], want[~bad]) <= GEMM_TOL
 
 
 CASES16 = ("skinny_m3", "skinny_m8", "gemm_m12", "gemm_m9", "skinny_tie16", "gemm_tie16")
