@@ -15,8 +15,9 @@ exactly as configured.
   each case runs on is the library's own report (g16_hgemm_tile), so a plan change that moves a
   case to another tile fails here instead of silently dropping that tile from the tests.
 * Rows holding +-inf or NaN (at tile-row edges and at K - 1), an all-zero row and rescaled rows
-  through the tile-packed route (both 256-row tiles, one round and persistent; fp32 and fp16 x and
-  out): exactly the oracle's non-finite pattern, every other row within the GEMM bar.
+  through the tile-packed route (both 256-row tiles, one round and persistent) and through every
+  4-wavefront route (split and unsplit, the resident cast), fp32 and fp16 x and out: exactly the
+  oracle's non-finite pattern, every other row within the GEMM bar.
 * The fp16-output golden fixtures (exact rational results, tests/golden/make_golden.py).
 
 Every result is checked against the fp64 oracle: relative Frobenius error <= 1e-3 on the GEMM
@@ -197,6 +198,56 @@ def test_packed_route_nonfinite_zero_and_rescaled_rows(g, lib, cus, cuda, M, K, 
         assert np.array_equal(np.isposinf(got), np.isposinf(want))
         assert np.array_equal(np.isneginf(got), np.isneginf(want))
         bad = np.isin(rows, list(special))
+        assert np.isnan(want[bad]).all() and np.isfinite(want[~bad]).all()
+        assert oracle.rel_err(got[~bad], want[~bad]) <= GEMM_TOL
+
+
+# (M, K, N, tile, ksplit, resident): the 4-wavefront routes. With fp32 x the cast is its own launch,
+# or, on the unsplit 32x128 tile with K <= 1280, the GEMM casts its rows into LDS (resident); with
+# fp16 x the GEMM streams x itself and recomputes the tiles whose rows exceed the threshold.
+SMALL_ROUTES = [
+    (48, 768, 1024, (32, 128), 1, True),
+    (64, 1024, 1024, (32, 128), 4, False),
+    (64, 4096, 1024, (32, 128), 8, False),
+    (1024, 1024, 1024, (64, 64), 1, False),
+    (320, 4056, 1024, (64, 64), 3, False),
+    (128, 8192, 4096, (64, 128), 4, False),
+    (768, 4056, 4096, (128, 128), 1, False),
+    (384, 4056, 3072, (128, 128), 3, False),
+]
+
+
+@pytest.mark.parametrize("M,K,N,tile,ks,resident", SMALL_ROUTES)
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.float16])
+def test_small_tile_routes_nonfinite_zero_and_rescaled_rows(g, lib, cus, cuda, M, K, N, tile, ks, resident, x_dtype):
+    # The same rows as on the packed route, on every 4-wavefront route: the split reduction adds
+    # the slices' NaN rows like any other, and no slice's non-finite row reaches another row.
+    if cus != 256:
+        pytest.skip(f"the route table is for 256 CUs (this device has {cus})")
+    assert planned_tile(lib, M, N, K, cus) == tile
+    assert lib.g16_hgemm_plan(M, N, K, cus) == ks
+    assert (lib.g16_mm_t_scratch_bytes(M, N, K, cus) == 0) == resident
+    x = randn((M, K), seed=41)
+    special = {1: ("inf", 7), 31: ("nan", 100), 32: ("inf", K - 1), M - 3: ("nan", 0), M - 2: ("-inf", K - 1),
+               M - 1: ("-inf", K // 2)}
+    assert len(special) == 6 and not {3, 10, 33} & set(special)
+    for r, (v, k) in special.items():
+        x[r, k] = float(v)
+    x[3] = 0.0           # an all-zero row
+    x[10, 3] = 3.0e4     # rescaled rows (exponent 5), fp16-representable
+    x[33, K - 1] = -2.5e4
+    x = x.to(x_dtype)
+    w = randn((K, N), seed=42, scale=0.02, dtype=torch.float16)
+    b = randn((N,), seed=43, scale=0.02)
+    for out_dtype, name in ((torch.float32, "float32"), (torch.float16, "float16")):
+        y = g.mm_t(x.to(cuda), w.to(cuda), b.to(cuda), out_dtype)
+        torch.cuda.synchronize()
+        got = _np(y).astype(np.float64)
+        want = oracle.mm_t(_np(x), _np(w), _np(b), name).astype(np.float64)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(np.isposinf(got), np.isposinf(want))
+        assert np.array_equal(np.isneginf(got), np.isneginf(want))
+        bad = np.isin(np.arange(M), list(special))
         assert np.isnan(want[bad]).all() and np.isfinite(want[~bad]).all()
         assert oracle.rel_err(got[~bad], want[~bad]) <= GEMM_TOL
 
