@@ -59,6 +59,32 @@ def test_mm_t_prepacked_bitwise_equals_mm_t(ops, cuda, M, K, N, out_dtype, in_dt
     assert oracle.rel_err(y.float().cpu().numpy(), ref.astype(np.float64)) <= 1e-3
 
 
+@pytest.mark.parametrize("M,K,N", [(2300, 264, 4096), (1800, 136, 3896)])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.float16])
+def test_mm_t_prepacked_nonfinite_rows_bitwise_equal_mm_t(ops, cuda, M, K, N, in_dtype):
+    # Rows holding +-inf or NaN (their output rows are NaN) on both 256-row tiles: the prepacked
+    # route gives mm_t's result bit for bit, NaN rows included, and the oracle's NaN rows.
+    assert ops.prepacked_route(M, N, K, cuda)
+    x = randn((M, K), seed=7)
+    for r, v, k in ((0, "inf", 5), (255, "nan", K - 1), (256, "-inf", 0), (M - 1, "nan", K // 2)):
+        x[r, k] = float(v)
+    x[700, 3] = 5e3  # a rescaled row
+    x = x.to(in_dtype).to(cuda)
+    w = randn((K, N), seed=8, scale=0.02, dtype=torch.float16).to(cuda)
+    bias = randn((N,), seed=9, scale=0.02).to(cuda)
+    wp = ops.pack_weight(w)
+    for out_dtype, view in ((torch.float32, torch.int32), (torch.float16, torch.int16)):
+        y0 = ops.mm_t(x, w, bias, out_dtype)
+        y1 = ops.mm_t_prepacked(x, w, wp, bias, out_dtype)
+        torch.cuda.synchronize()
+        assert torch.equal(y0.view(view), y1.view(view))
+        nan_rows = torch.isnan(y1).all(dim=1).cpu().numpy()
+        want = oracle.mm_t(x.cpu().numpy(), w.cpu().numpy(), bias.cpu().numpy(),
+                           "float32" if out_dtype == torch.float32 else "float16")
+        assert np.array_equal(nan_rows, np.isnan(want).all(axis=1))
+        assert nan_rows.sum() == 4 and torch.isfinite(y1[~torch.from_numpy(nan_rows).to(cuda)]).all()
+
+
 def test_mm_t_prepacked_off_route_is_mm_t(ops, cuda):
     # small and skinny shapes ignore wp and take mm_t's own route
     for M, K, N in [(300, 136, 264), (4, 1024, 1024)]:
