@@ -99,9 +99,9 @@ def gemm(y16, S, w16, bias=None, out_dtype: str = "float32") -> np.ndarray:
 
     The products of fp16 values are exact in fp64; the fp64 sum is the reference's ideal (its own
     hybrid fp16/fp32 accumulation is an approximation of it)."""
-    acc = np.asarray(y16, dtype=np.float64) @ np.asarray(w16, dtype=np.float64)
     S = np.asarray(S, dtype=np.float64)
-    with np.errstate(invalid="ignore", over="ignore"):
+    with np.errstate(invalid="ignore", over="ignore"):  # inf * 0 and inf - inf are NaN, as on the GPU
+        acc = np.asarray(y16, dtype=np.float64) @ np.asarray(w16, dtype=np.float64)
         out = acc * S[:, None]
         if bias is not None:
             out = out + np.asarray(bias, dtype=np.float64)[None, :]
@@ -112,9 +112,10 @@ def skinny(x, w16, bias=None, out_dtype: str = "float32") -> np.ndarray:
     """Skinny path (M <= 8) of kernels.py:160-219, ops.py:78-84: fp32 math on the UNQUANTISED
     activations (fp32 or fp16 used as is), fp16 weights, bias added once; fp32 out, or its
     nearest-even fp16 (``out.to(fp16)``, ops.py:84)."""
-    out = np.asarray(x, dtype=np.float64) @ np.asarray(w16, dtype=np.float64)
-    if bias is not None:
-        out = out + np.asarray(bias, dtype=np.float64)[None, :]
+    with np.errstate(invalid="ignore", over="ignore"):
+        out = np.asarray(x, dtype=np.float64) @ np.asarray(w16, dtype=np.float64)
+        if bias is not None:
+            out = out + np.asarray(bias, dtype=np.float64)[None, :]
     if out_dtype in ("float16", "f16", np.float16):
         return fp16_rne(out.astype(np.float32))
     return _out_cast(out, out_dtype)

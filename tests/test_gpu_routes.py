@@ -252,6 +252,46 @@ def test_small_tile_routes_nonfinite_zero_and_rescaled_rows(g, lib, cus, cuda, M
         assert oracle.rel_err(got[~bad], want[~bad]) <= GEMM_TOL
 
 
+WEIGHT_ROUTES = [(M, K, N) for (M, K, N, *_r) in SMALL_ROUTES] + [
+    (2600, 2056, 2824),   # packed 256x256, one round
+    (4096, 1032, 4104),   # packed 256x256, persistent grid
+    (2048, 2056, 3080),   # packed 256x128
+]
+
+
+@pytest.mark.parametrize("M,K,N", WEIGHT_ROUTES)
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.float16])
+def test_nonfinite_weights_on_every_route(g, lib, cus, cuda, M, K, N, x_dtype):
+    # Weight columns holding +inf (at k = 0), -inf (at K - 1, in the last K step and slice) and NaN
+    # (mid-K), and a column holding +inf and -inf: each output entry is +-inf by the sign of the
+    # activation it meets, NaN where that activation is exactly zero or the column's infinities
+    # cancel, the oracle's pattern exactly; the other columns are untouched.
+    if cus != 256:
+        pytest.skip(f"the route table is for 256 CUs (this device has {cus})")
+    x = randn((M, K), seed=51)
+    x[5, 0] = 0.0          # inf * 0 -> NaN in row 5 of the +inf column
+    x[9, K - 1] = 0.0
+    x[12, 3] = 4.0e4       # a rescaled row
+    x = x.to(x_dtype)
+    w = randn((K, N), seed=52, scale=0.02, dtype=torch.float16)
+    cols = {3: (0, "inf"), N // 2: (K - 1, "-inf"), N - 1: (K // 2, "nan")}
+    for c, (k, v) in cols.items():
+        w[k, c] = float(v)
+    w[1, 7], w[K - 2, 7] = float("inf"), float("-inf")
+    b = randn((N,), seed=53, scale=0.02)
+    for out_dtype, name in ((torch.float32, "float32"), (torch.float16, "float16")):
+        y = g.mm_t(x.to(cuda), w.to(cuda), b.to(cuda), out_dtype)
+        torch.cuda.synchronize()
+        got = _np(y).astype(np.float64)
+        want = oracle.mm_t(_np(x), _np(w), _np(b), name).astype(np.float64)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(np.isposinf(got), np.isposinf(want))
+        assert np.array_equal(np.isneginf(got), np.isneginf(want))
+        special = np.isin(np.arange(N), list(cols) + [7])
+        assert not np.isfinite(want[:, special]).any() and np.isnan(want[5, 3]) and np.isnan(want[9, N // 2])
+        assert oracle.rel_err(got[:, ~special], want[:, ~special]) <= GEMM_TOL
+
+
 CASES16 = ("skinny_m3", "skinny_m8", "gemm_m12", "gemm_m9", "skinny_tie16", "gemm_tie16")
 
 
