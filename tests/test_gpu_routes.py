@@ -16,8 +16,9 @@ exactly as configured.
   case to another tile fails here instead of silently dropping that tile from the tests.
 * Rows holding +-inf or NaN (at tile-row edges and at K - 1), an all-zero row and rescaled rows
   through the tile-packed route (both 256-row tiles, one round and persistent) and through every
-  4-wavefront route (split and unsplit, the resident cast), fp32 and fp16 x and out: exactly the
-  oracle's non-finite pattern, every other row within the GEMM bar.
+  4-wavefront route (split and unsplit, the resident cast), fp32 and fp16 x and out; likewise weight
+  columns holding +-inf and NaN (at k = 0, mid-K and K - 1) against exact-zero activations: exactly
+  the oracle's non-finite pattern, every other row and column within the GEMM bar.
 * The fp16-output golden fixtures (exact rational results, tests/golden/make_golden.py).
 
 Every result is checked against the fp64 oracle: relative Frobenius error <= 1e-3 on the GEMM
