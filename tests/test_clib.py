@@ -2,6 +2,7 @@
 rejects bad arguments before any launch (so these calls need no GPU)."""
 from __future__ import annotations
 
+import ctypes
 import re
 from pathlib import Path
 
@@ -24,6 +25,58 @@ def lib():
 
 def test_header_and_binding_agree():
     assert declared_functions() == set(_clib.SIGNATURES)
+
+
+_CTYPE = {"int": ctypes.c_int, "float": ctypes.c_float, "double": ctypes.c_double, "size_t": ctypes.c_size_t}
+
+
+def _ctype(decl: str, ret: bool = False):
+    # a C parameter or return type of the header as the ctypes type that passes it: any pointer is
+    # c_void_p (c_char_p for the strerror string), the scalars by name
+    decl = decl.strip()
+    if "*" in decl:
+        return ctypes.c_char_p if ret and "char" in decl else ctypes.c_void_p
+    words = [w for w in decl.split() if w != "const"]
+    base = words[0] if ret else " ".join(words[:-1])
+    return _CTYPE[base]
+
+
+def header_prototypes() -> dict[str, tuple[object, list[object]]]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"#.*", "", text)
+    out = {}
+    for ret, name, args in re.findall(r"([\w\s\*]+?)\b(g16_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [a for a in (s.strip() for s in args.split(",")) if a and a != "void"]
+        out[name] = (_ctype(ret, ret=True), [_ctype(p) for p in params])
+    return out
+
+
+def test_binding_types_match_the_header_prototypes():
+    # every argument and result type the ctypes binding declares is the one the C prototype has
+    # (a size_t bound as c_int, say, would pass the low half of the register and garbage above it)
+    protos = header_prototypes()
+    assert set(protos) == set(_clib.SIGNATURES)
+    for name, (res, args) in _clib.SIGNATURES.items():
+        assert protos[name] == (res, args), name
+
+
+def test_integration_ctypes_stub_matches_the_binding():
+    # the stub INTEGRATION.md shows a maintainer (route 2) binds the same types as this package
+    doc = (HEADER.parents[1] / "INTEGRATION.md").read_text()
+    block = doc.split("# src/gtx16_fp16/_rocm.py")[1].split("```")[0]
+    alias = {"P": ctypes.c_void_p, "I": ctypes.c_int, "F": ctypes.c_float, "SZ": ctypes.c_size_t}
+    seen = {}
+    for name, args in re.findall(r'"(g16_\w+)":\s*\[([^\]]*)\]', block):
+        seen[name] = [alias[a.strip()] for a in args.split(",") if a.strip()]
+    for names, args in re.findall(r"for name in \(([^)]*)\):\s*\n\s*fn = getattr\(_lib, name\); "
+                                  r"fn\.argtypes, fn\.restype = \[([^\]]*)\]", block):
+        for name in re.findall(r'"(g16_\w+)"', names):
+            seen[name] = [alias[a.strip()] for a in args.split(",")]
+    for name, args in re.findall(r"_lib\.(g16_\w+)\.argtypes, _lib\.\1\.restype = \[([^\]]*)\]", block):
+        seen[name] = [alias[a.strip()] for a in args.split(",")]
+    assert len(seen) >= 14
+    for name, args in seen.items():
+        assert args == list(_clib.SIGNATURES[name][1]), name
 
 
 def test_library_exports_every_declared_symbol(lib):
