@@ -19,6 +19,13 @@ def g(cuda):
     return gtx16_fp16
 
 
+@pytest.fixture(scope="module")
+def lib(cuda):
+    from gtx16_fp16 import _clib
+
+    return _clib.load()
+
+
 def _ref_linear(x: torch.Tensor, fl) -> np.ndarray:
     x2 = x.detach().reshape(-1, fl.in_features).float().cpu().numpy()
     w = fl.weight_t.cpu().numpy()
@@ -206,6 +213,45 @@ def test_graph_capture_replays_match_eager(g, cuda):
             assert torch.equal(out, eager), i
             with torch.no_grad():
                 assert torch.equal(fl(x), eager)
+
+
+def test_graph_of_every_mm_t_route_replays_bitwise(g, lib, cuda):
+    # One graph holding mm_t on every route: the tile-packed 256x256 GEMM in one round and as a
+    # persistent grid (cast + GEMM), the one-launch fp16 route, the resident one-launch fp32 route,
+    # and the skinny kernel at M = 4 (FMA loop) and M = 8 (matrix cores). Replayed several times with
+    # other eager mm_t work in between, every replay must equal the eager results bit for bit.
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    cases = [(2304, 256, 4096, torch.float32), (2560, 512, 8192, torch.float32), (1024, 1024, 1024, torch.float16),
+             (48, 768, 1024, torch.float32), (4, 4096, 4096, torch.float32), (8, 4096, 4096, torch.float32)]
+    if cus == 256:
+        assert lib.g16_hgemm_use_packed(2304, 4096, 256, cus) == 1 and lib.g16_hgemm_use_packed(2560, 8192, 512, cus) == 1
+        assert lib.g16_mm_t_scratch_bytes(48, 1024, 768, cus) == 0  # the resident route
+    gens = [torch.Generator(cuda).manual_seed(70 + i) for i in range(len(cases))]
+    xs = [torch.randn(M, K, device=cuda, generator=gn).to(dt) for (M, K, N, dt), gn in zip(cases, gens)]
+    for x in xs[:2]:
+        x[7] *= 3000.0  # a rescaled row on the packed route
+    ws = [(torch.randn(K, N, device=cuda, generator=gn) * 0.02).half() for (M, K, N, dt), gn in zip(cases, gens)]
+    bs = [torch.randn(N, device=cuda, generator=gn) * 0.02 for (M, K, N, dt), gn in zip(cases, gens)]
+    eager = [g.mm_t(x, w, b, torch.float32) for x, w, b in zip(xs, ws, bs)]
+    s = torch.cuda.Stream(cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(s):
+        for x, w, b in zip(xs, ws, bs):
+            g.mm_t(x, w, b, torch.float32)  # eager on the capture stream first: its buffers exist
+    s.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        outs = [g.mm_t(x, w, b, torch.float32) for x, w, b in zip(xs, ws, bs)]
+    other_x = torch.randn(300, 512, device=cuda)
+    other_w = (torch.randn(512, 384, device=cuda) * 0.02).half()
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        for k, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o, e), (i, cases[k][:3])
+        g.mm_t(other_x, other_w)  # the program's own eager work between replays
+        g.mm_t(xs[4], ws[4], bs[4])
+        torch.cuda.synchronize()
 
 
 def test_graphs_of_mm_t_keep_their_buffers_when_a_later_capture_outgrows_them(g, cuda):
