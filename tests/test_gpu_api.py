@@ -298,6 +298,8 @@ def test_graphs_of_mm_t_keep_their_buffers_when_a_later_capture_outgrows_them(g,
 @pytest.mark.parametrize("shapes", [
     ((64, 4096, 1024, torch.float16), (64, 4096, 1024, torch.float16)),  # one split-K route on both
     ((64, 4096, 1024, torch.float32), (4, 4096, 4096, torch.float32)),  # split-K cast + GEMM; skinny
+    ((2304, 256, 4096, torch.float32), (8, 4096, 4096, torch.float32)),  # packed cast + GEMM; skinny (matrix cores)
+    ((2560, 512, 8192, torch.float32), (2560, 512, 8192, torch.float32)),  # the persistent packed grid on both
 ])
 def test_concurrent_streams_keep_their_own_split_buffers(g, cuda, shapes):
     # Calls on different streams may run at the same time, so each stream has its own split
